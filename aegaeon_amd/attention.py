@@ -1,0 +1,210 @@
+"""Token-level KV ops with the vLLM 0.5.1 surface the reference reaches from
+its model forward (aegaeon/aegaeon/worker.py:517-523):
+
+* :func:`reshape_and_cache_flash` — vLLM's per-layer K/V append into the
+  flash-attn cache view ``[N, 16, Hkv, D]``;
+* :func:`append_kv` — the same append for every layer of the reference's
+  ``[N, L, 2, 16, Hkv, D]`` storage (worker.py:389-395) in one launch;
+* :func:`gather_tokens` — block-table de-page into contiguous buffers;
+* :func:`flash_attn_with_kvcache` — vllm-flash-attn's paged decode call
+  (selected at worker.py:410-418) for one query token per sequence.
+
+All of them enqueue hand-written gfx950 kernels on the current torch stream.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.AEGKV_DTYPE_BF16, torch.float16: _lib.AEGKV_DTYPE_FP16}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check_cache_view(c: torch.Tensor, name: str) -> None:
+    """A per-layer cache view ``[N, bs, Hkv, D]`` with dense rows per block."""
+    if c.dim() != 4 or not c.is_cuda:
+        raise ValueError(f"{name} must be a 4-d GPU tensor [N, block_size, Hkv, D]")
+    N, bs, H, D = c.shape
+    if c.stride(3) != 1 or c.stride(2) != D or c.stride(1) != H * D:
+        raise ValueError(f"{name}: each block must hold dense [block_size, Hkv, D] rows")
+
+
+def _check_rows(x: torch.Tensor, name: str) -> None:
+    if not x.is_cuda or x.stride(-1) != 1 or x.stride(-2) != x.size(-1):
+        raise ValueError(f"{name}: rows [Hkv, D] must be dense on the GPU")
+
+
+def reshape_and_cache_flash(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                            value_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                            kv_cache_dtype: str = "auto") -> None:
+    """For token t with ``s = slot_mapping[t] >= 0``:
+    ``key_cache[s // bs, s % bs] = key[t]`` and likewise for V.
+
+    key/value: ``[T, Hkv, D]`` (token stride may exceed Hkv*D);
+    key_cache/value_cache: ``[N, bs, Hkv, D]`` views with any block stride;
+    slot_mapping: int64 GPU tensor ``[T]``.  Only ``kv_cache_dtype="auto"``
+    (the reference's setting, aegaeon/aegaeon/models.py:384-390) is supported.
+    """
+    if kv_cache_dtype != "auto":
+        raise NotImplementedError("only kv_cache_dtype='auto' is supported")
+    _check_cache_view(key_cache, "key_cache")
+    _check_cache_view(value_cache, "value_cache")
+    _check_rows(key, "key")
+    _check_rows(value, "value")
+    if key_cache.stride(0) != value_cache.stride(0):
+        raise ValueError("key_cache and value_cache must share the block stride")
+    if slot_mapping.dtype != torch.int64 or not slot_mapping.is_cuda:
+        raise ValueError("slot_mapping must be an int64 GPU tensor")
+    T = key.size(0)
+    N, bs, H, D = key_cache.shape
+    slot_mapping = slot_mapping.contiguous()
+    with torch.cuda.device(key.device):
+        rc = _lib.load().aegkv_kv_append(
+            key.data_ptr(), value.data_ptr(), key.stride(0), value.stride(0), 0, 0,
+            slot_mapping.data_ptr(), T, key_cache.data_ptr(), value_cache.data_ptr(),
+            key_cache.stride(0), 0, N, 1, bs, H, D, key.element_size(), _stream(key))
+    _lib.check(rc, "reshape_and_cache_flash")
+
+
+def append_kv(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+              slot_mapping: torch.Tensor) -> None:
+    """Append one decode step for every layer in one launch.
+
+    key/value: ``[L, T, Hkv, D]`` (dense rows; token and layer strides free);
+    kv_cache: the reference's contiguous storage ``[N, L, 2, bs, Hkv, D]``.
+    """
+    if kv_cache.dim() != 6 or not kv_cache.is_contiguous() or not kv_cache.is_cuda:
+        raise ValueError("kv_cache must be a contiguous GPU tensor [N, L, 2, bs, Hkv, D]")
+    N, L, two, bs, H, D = kv_cache.shape
+    if key.dim() != 4 or key.size(0) != L or key.shape[2:] != (H, D) or value.shape != key.shape:
+        raise ValueError("key/value must be [L, T, Hkv, D] matching the cache")
+    _check_rows(key, "key")
+    _check_rows(value, "value")
+    if slot_mapping.dtype != torch.int64 or not slot_mapping.is_cuda:
+        raise ValueError("slot_mapping must be an int64 GPU tensor")
+    slot_mapping = slot_mapping.contiguous()
+    T = key.size(1)
+    kv_stride = bs * H * D
+    with torch.cuda.device(kv_cache.device):
+        base = kv_cache.data_ptr()
+        rc = _lib.load().aegkv_kv_append(
+            key.data_ptr(), value.data_ptr(), key.stride(1), value.stride(1), key.stride(0),
+            value.stride(0), slot_mapping.data_ptr(), T, base,
+            base + kv_stride * kv_cache.element_size(), kv_cache.stride(0), kv_cache.stride(1), N,
+            L, bs, H, D, kv_cache.element_size(), _stream(kv_cache))
+    _lib.check(rc, "append_kv")
+
+
+def gather_tokens(kv_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: torch.Tensor,
+                  total_tokens: int, max_seq_len: int, layers: Optional[Tuple[int, int]] = None,
+                  cu_seqlens: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """De-page sequences: returns ``(out_k, out_v)`` of shape
+    ``[n_layers, total_tokens, Hkv, D]`` with sequence b's tokens at
+    ``cu_seqlens[b] : cu_seqlens[b] + seq_lens[b]``.
+
+    kv_cache: storage ``[N, L, 2, bs, Hkv, D]``; block_tables int32
+    ``[B, max_blocks]`` (0-padded like worker.py:640-646); seq_lens int32 [B];
+    total_tokens and max_seq_len: host-side sum and maximum of seq_lens;
+    layers: ``(first, count)`` (default all).
+    """
+    if kv_cache.dim() != 6 or not kv_cache.is_contiguous() or not kv_cache.is_cuda:
+        raise ValueError("kv_cache must be a contiguous GPU tensor [N, L, 2, bs, Hkv, D]")
+    N, L, _, bs, H, D = kv_cache.shape
+    first, count = layers if layers is not None else (0, L)
+    if not (0 <= first and first + count <= L and count > 0):
+        raise ValueError("layer range out of bounds")
+    bt = block_tables.to(torch.int32).contiguous()
+    sl = seq_lens.to(torch.int32).contiguous()
+    if cu_seqlens is None:
+        cu_seqlens = torch.zeros(sl.numel() + 1, dtype=torch.int32, device=sl.device)
+        torch.cumsum(sl, 0, dtype=torch.int32, out=cu_seqlens[1:])
+    out_k = torch.empty((count, total_tokens, H, D), dtype=kv_cache.dtype, device=kv_cache.device)
+    out_v = torch.empty_like(out_k)
+    if total_tokens == 0:
+        return out_k, out_v
+    es = kv_cache.element_size()
+    with torch.cuda.device(kv_cache.device):
+        base = kv_cache.data_ptr() + first * kv_cache.stride(1) * es
+        rc = _lib.load().aegkv_gather_tokens(
+            base, base + bs * H * D * es, kv_cache.stride(0), kv_cache.stride(1), N,
+            bt.data_ptr(), bt.size(1), sl.data_ptr(), cu_seqlens.data_ptr(), sl.numel(),
+            max_seq_len, out_k.data_ptr(), out_v.data_ptr(), total_tokens, total_tokens * H * D,
+            count, bs, H, D, es, _stream(kv_cache))
+    _lib.check(rc, "gather_tokens")
+    return out_k, out_v
+
+
+def attention_workspace_bytes(batch: int, n_q_heads: int, head_dim: int, max_seq_len: int,
+                              blocks_per_split: int = 0, block_size: int = 16) -> int:
+    n = _lib.load().aegkv_paged_decode_attention_workspace_size(
+        batch, n_q_heads, head_dim, max_seq_len, block_size, blocks_per_split)
+    if n < 0:
+        _lib.check(int(n), "attention_workspace_bytes")
+    return int(n)
+
+
+def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                           block_tables: torch.Tensor, seq_lens: torch.Tensor, scale: float,
+                           max_seq_len: int, out: Optional[torch.Tensor] = None,
+                           blocks_per_split: int = 0,
+                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Paged GQA decode attention: ``q [B, Hq, D]`` against per-layer cache
+    views ``[N, 16, Hkv, D]``; returns ``out [B, Hq, D]`` in q's dtype."""
+    if q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.size(2) or not q.is_cuda:
+        raise ValueError("q must be a GPU tensor [B, Hq, D] with dense heads")
+    _check_cache_view(key_cache, "key_cache")
+    _check_cache_view(value_cache, "value_cache")
+    if key_cache.stride(0) != value_cache.stride(0):
+        raise ValueError("key_cache and value_cache must share the block stride")
+    if q.dtype not in _DTYPES or key_cache.dtype != q.dtype or value_cache.dtype != q.dtype:
+        raise ValueError("q, key_cache and value_cache must share a bf16/fp16 dtype")
+    B, Hq, D = q.shape
+    N, bs, Hkv, _ = key_cache.shape
+    bt = block_tables if (block_tables.dtype == torch.int32 and block_tables.is_contiguous()) \
+        else block_tables.to(torch.int32).contiguous()
+    sl = seq_lens if (seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()) \
+        else seq_lens.to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    elif out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D:
+        raise ValueError("out must be [B, Hq, D] with dense heads")
+    ws_bytes = attention_workspace_bytes(B, Hq, D, max_seq_len, blocks_per_split, bs)
+    if ws_bytes > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if (workspace is not None and ws_bytes > 0) else None
+    with torch.cuda.device(q.device):
+        rc = _lib.load().aegkv_paged_decode_attention(
+            out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), key_cache.data_ptr(),
+            value_cache.data_ptr(), key_cache.stride(0), N, bt.data_ptr(), bt.size(1),
+            sl.data_ptr(), B, max_seq_len, Hq, Hkv, D, bs, float(scale), _DTYPES[q.dtype],
+            blocks_per_split, ws_ptr, ws_bytes if ws_ptr else 0, _stream(q))
+    _lib.check(rc, "paged_decode_attention")
+    return out
+
+
+def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                            block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+                            softmax_scale: Optional[float] = None, causal: bool = True,
+                            max_seqlen: Optional[int] = None,
+                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """vllm-flash-attn's paged decode call for one query token per sequence:
+    ``q [B, 1, Hq, D]`` -> ``[B, 1, Hq, D]``.  With a single query token the
+    causal mask admits every cached token, so ``causal`` does not change the
+    result.  ``max_seqlen`` (host bound of cache_seqlens) defaults to
+    ``block_table.size(1) * block_size``."""
+    if q.dim() != 4 or q.size(1) != 1:
+        raise NotImplementedError("decode only: q must be [B, 1, Hq, D]")
+    B, _, Hq, D = q.shape
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    bs = k_cache.size(1)
+    ms = max_seqlen if max_seqlen is not None else block_table.size(1) * bs
+    o = paged_decode_attention(q.view(B, Hq, D), k_cache, v_cache, block_table, cache_seqlens,
+                               scale, ms, out=None if out is None else out.view(B, Hq, D))
+    return o.view(B, 1, Hq, D)

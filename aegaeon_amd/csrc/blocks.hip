@@ -1,0 +1,266 @@
+// Block-granular KV movement on gfx950: gather (pack), scatter, pool-to-pool
+// copy, defrag and the CPU<->GPU swap that replaces aegaeon.ops.swap
+// (aegaeon/ops/swap.cu:25-59).
+//
+// One kernel serves every device-side move.  A block of block_bytes is cut into
+// 16 KiB tiles; a 256-thread workgroup moves one tile per iteration with four
+// dwordx4 (16 B) loads per lane issued before the four stores, so each wave
+// keeps 4 KiB in flight and every access is a fully coalesced 1 KiB wave row.
+// The grid is persistent (a few workgroups per CU) and strides over tiles.
+#include <algorithm>
+#include <numeric>
+
+#include "aegkv_internal.h"
+
+namespace aegkv {
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 4;
+constexpr uint64_t kTileBytes = (uint64_t)kCopyThreads * 16 * kCopyUnroll;  // 16 KiB
+
+__global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
+    const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+    const int64_t* __restrict__ src_ids, const int64_t* __restrict__ dst_ids,
+    uint64_t block_bytes, uint32_t tiles_per_block, uint64_t n_tiles) {
+  for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    const uint64_t i = tile / tiles_per_block;
+    const uint64_t t = tile - i * tiles_per_block;
+    const int64_t s = src_ids ? src_ids[i] : (int64_t)i;
+    const int64_t d = dst_ids ? dst_ids[i] : (int64_t)i;
+    const uint64_t base = t * kTileBytes;
+    const uint64_t rem = block_bytes - base;  // bytes of this block from the tile start
+    const u32x4* sp = reinterpret_cast<const u32x4*>(src + (uint64_t)s * block_bytes + base);
+    u32x4* dp = reinterpret_cast<u32x4*>(dst + (uint64_t)d * block_bytes + base);
+    u32x4 r[kCopyUnroll];
+#pragma unroll
+    for (int k = 0; k < kCopyUnroll; ++k) {
+      const uint32_t c = k * kCopyThreads + threadIdx.x;
+      if ((uint64_t)c * 16 < rem) r[k] = __builtin_nontemporal_load(sp + c);
+    }
+#pragma unroll
+    for (int k = 0; k < kCopyUnroll; ++k) {
+      const uint32_t c = k * kCopyThreads + threadIdx.x;
+      if ((uint64_t)c * 16 < rem) __builtin_nontemporal_store(r[k], dp + c);
+    }
+  }
+}
+
+}  // namespace
+
+int launch_copy_blocks(const DeviceState* ds, const void* src, void* dst,
+                       const int64_t* src_ids_dev, const int64_t* dst_ids_dev,
+                       int64_t n, uint64_t block_bytes, hipStream_t stream) {
+  if (n <= 0) return AEGKV_OK;
+  const uint64_t tiles_per_block = (block_bytes + kTileBytes - 1) / kTileBytes;
+  const uint64_t n_tiles = tiles_per_block * (uint64_t)n;
+  const uint64_t max_grid = (uint64_t)std::max(ds->num_cu, 1) * 8;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, max_grid);
+  hipLaunchKernelGGL(copy_blocks_kernel, dim3(grid), dim3(kCopyThreads), 0, stream,
+                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst),
+                     src_ids_dev, dst_ids_dev, block_bytes, (uint32_t)tiles_per_block,
+                     n_tiles);
+  AEGKV_HIP_TRY(hipGetLastError());
+  return AEGKV_OK;
+}
+
+namespace {
+
+bool ranges_overlap(const void* a, uint64_t na, const void* b, uint64_t nb) {
+  auto x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + nb && y < x + na;
+}
+
+// Shared body of copy/pack/scatter/defrag: validate on the host, upload the id
+// lists, launch one copy kernel.
+int copy_blocks_checked(const void* src_pool, uint64_t n_src_blocks, void* dst_pool,
+                        uint64_t n_dst_blocks, const int64_t* src_ids,
+                        const int64_t* dst_ids, int64_t n, uint64_t block_bytes,
+                        bool require_same_pool, hipStream_t stream) {
+  if (n < 0 || !src_pool || !dst_pool || block_bytes == 0) return AEGKV_ERR_INVALID_ARG;
+  if (n == 0) return AEGKV_OK;
+  if ((block_bytes & 15) || !aligned16(src_pool) || !aligned16(dst_pool))
+    return AEGKV_ERR_MISALIGNED;
+  int rc;
+  if (src_ids) {
+    if ((rc = check_ids_in_range(src_ids, n, n_src_blocks))) return rc;
+  } else if ((uint64_t)n > n_src_blocks) {
+    return AEGKV_ERR_OUT_OF_RANGE;
+  }
+  if (dst_ids) {
+    if ((rc = check_ids_in_range(dst_ids, n, n_dst_blocks))) return rc;
+    if ((rc = check_unique(dst_ids, n))) return rc;
+  } else if ((uint64_t)n > n_dst_blocks) {
+    return AEGKV_ERR_OUT_OF_RANGE;
+  }
+  const bool same = src_pool == dst_pool;
+  if (require_same_pool && !same) return AEGKV_ERR_INVALID_ARG;
+  if (same) {
+    // In-place moves must not read a block another lane writes.
+    std::vector<int64_t> s, d;
+    if (!src_ids) { s.resize(n); std::iota(s.begin(), s.end(), 0); }
+    if (!dst_ids) { d.resize(n); std::iota(d.begin(), d.end(), 0); }
+    if ((rc = check_disjoint(src_ids ? src_ids : s.data(), n, dst_ids ? dst_ids : d.data(), n)))
+      return rc;
+  } else if (ranges_overlap(src_pool, n_src_blocks * block_bytes, dst_pool,
+                            n_dst_blocks * block_bytes)) {
+    return AEGKV_ERR_OVERLAP;  // partially aliased pools: order would matter
+  }
+  DeviceState* ds = nullptr;
+  if ((rc = current_device_state(&ds))) return rc;
+  IdPart parts[2] = {{src_ids, src_ids ? n : 0}, {dst_ids, dst_ids ? n : 0}};
+  return with_uploaded_ids(ds, stream, parts, 2, [&](int64_t* dev) {
+    const int64_t* s = src_ids ? dev : nullptr;
+    const int64_t* d = dst_ids ? dev + (src_ids ? n : 0) : nullptr;
+    return launch_copy_blocks(ds, src_pool, dst_pool, s, d, n, block_bytes, stream);
+  });
+}
+
+// Maximal runs [i, j) of `order` over which key[order[k]] increases by one.
+template <typename F>
+void for_each_run(const std::vector<int64_t>& order, const int64_t* key, int64_t begin,
+                  int64_t end, F&& f) {
+  int64_t i = begin;
+  while (i < end) {
+    int64_t j = i + 1;
+    while (j < end && key[order[j]] == key[order[j - 1]] + 1) ++j;
+    f(i, j);
+    i = j;
+  }
+}
+
+}  // namespace
+}  // namespace aegkv
+
+using namespace aegkv;
+
+extern "C" {
+
+int aegkv_copy_blocks(const void* src_pool, uint64_t n_src_blocks, void* dst_pool,
+                      uint64_t n_dst_blocks, const int64_t* src_ids,
+                      const int64_t* dst_ids, int64_t n, uint64_t block_bytes,
+                      aegkv_stream_t stream) {
+  return copy_blocks_checked(src_pool, n_src_blocks, dst_pool, n_dst_blocks, src_ids,
+                             dst_ids, n, block_bytes, false, (hipStream_t)stream);
+}
+
+int aegkv_pack_blocks(const void* pool, uint64_t n_pool_blocks, const int64_t* ids,
+                      int64_t n, void* staging, uint64_t block_bytes,
+                      aegkv_stream_t stream) {
+  if (!ids && n > 0) return AEGKV_ERR_INVALID_ARG;
+  return copy_blocks_checked(pool, n_pool_blocks, staging, n > 0 ? (uint64_t)n : 0, ids,
+                             nullptr, n, block_bytes, false, (hipStream_t)stream);
+}
+
+int aegkv_scatter_blocks(const void* staging, const int64_t* ids, int64_t n, void* pool,
+                         uint64_t n_pool_blocks, uint64_t block_bytes,
+                         aegkv_stream_t stream) {
+  if (!ids && n > 0) return AEGKV_ERR_INVALID_ARG;
+  return copy_blocks_checked(staging, n > 0 ? (uint64_t)n : 0, pool, n_pool_blocks,
+                             nullptr, ids, n, block_bytes, false, (hipStream_t)stream);
+}
+
+int aegkv_defrag_blocks(void* pool, uint64_t n_pool_blocks, const int64_t* src_ids,
+                        const int64_t* dst_ids, int64_t n, uint64_t block_bytes,
+                        aegkv_stream_t stream) {
+  if ((!src_ids || !dst_ids) && n > 0) return AEGKV_ERR_INVALID_ARG;
+  return copy_blocks_checked(pool, n_pool_blocks, pool, n_pool_blocks, src_ids, dst_ids, n,
+                             block_bytes, true, (hipStream_t)stream);
+}
+
+int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+                      int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
+                      void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
+                      void* staging, uint64_t staging_bytes, aegkv_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  if (n < 0 || !dev_pool || !host_pool || block_bytes == 0) return AEGKV_ERR_INVALID_ARG;
+  if (n == 0) return AEGKV_OK;
+  if (!src_ids || !dst_ids) return AEGKV_ERR_INVALID_ARG;
+  const uint64_t n_src = is_swap_in ? n_host_blocks : n_dev_blocks;
+  const uint64_t n_dst = is_swap_in ? n_dev_blocks : n_host_blocks;
+  int rc;
+  if ((rc = check_ids_in_range(src_ids, n, n_src))) return rc;
+  if ((rc = check_ids_in_range(dst_ids, n, n_dst))) return rc;
+  if ((rc = check_unique(dst_ids, n))) return rc;
+
+  uint8_t* dev = static_cast<uint8_t*>(dev_pool);
+  uint8_t* host = static_cast<uint8_t*>(host_pool);
+  const uint64_t bb = block_bytes;
+  // Host-side order: sort the pairs by their host block id so that runs of
+  // consecutive host ids become single DMAs.
+  const int64_t* host_key = is_swap_in ? src_ids : dst_ids;
+  std::vector<int64_t> order(n);
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int64_t a, int64_t b) { return host_key[a] < host_key[b]; });
+
+  const bool staged = staging && staging_bytes >= bb;
+  if (!staged) {
+    // One DMA per run where both ids advance by one (the reference issues one
+    // cudaMemcpyAsync per block, swap.cu:36-58).
+    int64_t i = 0;
+    while (i < n) {
+      int64_t j = i + 1;
+      while (j < n && src_ids[order[j]] == src_ids[order[j - 1]] + 1 &&
+             dst_ids[order[j]] == dst_ids[order[j - 1]] + 1)
+        ++j;
+      const uint64_t bytes = (uint64_t)(j - i) * bb;
+      const uint64_t so = (uint64_t)src_ids[order[i]] * bb, dof = (uint64_t)dst_ids[order[i]] * bb;
+      if (is_swap_in)
+        AEGKV_HIP_TRY(hipMemcpyAsync(dev + dof, host + so, bytes, hipMemcpyHostToDevice, stream));
+      else
+        AEGKV_HIP_TRY(hipMemcpyAsync(host + dof, dev + so, bytes, hipMemcpyDeviceToHost, stream));
+      i = j;
+    }
+    return AEGKV_OK;
+  }
+  if ((bb & 15) || !aligned16(dev_pool) || !aligned16(staging)) return AEGKV_ERR_MISALIGNED;
+
+  DeviceState* ds = nullptr;
+  if ((rc = current_device_state(&ds))) return rc;
+  uint8_t* stg = static_cast<uint8_t*>(staging);
+  const int64_t cap = (int64_t)std::min<uint64_t>(staging_bytes / bb, (uint64_t)n);
+  std::vector<int64_t> dev_ids(cap);
+  for (int64_t c0 = 0; c0 < n; c0 += cap) {
+    const int64_t m = std::min(cap, n - c0);
+    const int64_t* dev_key = is_swap_in ? dst_ids : src_ids;
+    for (int64_t k = 0; k < m; ++k) dev_ids[k] = dev_key[order[c0 + k]];
+    IdPart part{dev_ids.data(), m};
+    if (!is_swap_in) {
+      // gather scattered device blocks into staging, then DMA each host run
+      rc = with_uploaded_ids(ds, stream, &part, 1, [&](int64_t* ids) {
+        return launch_copy_blocks(ds, dev, stg, ids, nullptr, m, bb, stream);
+      });
+      if (rc) return rc;
+      int err = 0;
+      for_each_run(order, dst_ids, c0, c0 + m, [&](int64_t i, int64_t j) {
+        if (err) return;
+        hipError_t e = hipMemcpyAsync(host + (uint64_t)dst_ids[order[i]] * bb,
+                                      stg + (uint64_t)(i - c0) * bb, (uint64_t)(j - i) * bb,
+                                      hipMemcpyDeviceToHost, stream);
+        if (e != hipSuccess) err = (int)e;
+      });
+      if (err) return err;
+    } else {
+      // DMA each host run into staging, then scatter to the device blocks
+      int err = 0;
+      for_each_run(order, src_ids, c0, c0 + m, [&](int64_t i, int64_t j) {
+        if (err) return;
+        hipError_t e = hipMemcpyAsync(stg + (uint64_t)(i - c0) * bb,
+                                      host + (uint64_t)src_ids[order[i]] * bb,
+                                      (uint64_t)(j - i) * bb, hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) err = (int)e;
+      });
+      if (err) return err;
+      rc = with_uploaded_ids(ds, stream, &part, 1, [&](int64_t* ids) {
+        return launch_copy_blocks(ds, stg, dev, nullptr, ids, m, bb, stream);
+      });
+      if (rc) return rc;
+    }
+  }
+  return AEGKV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,171 @@
+// Library runtime: status strings, version, per-device state and the id upload
+// ring used to hand host id lists (the reference's std::vector<int64_t>
+// arguments, aegaeon/ops/ops.h:4-10) to the block kernels without blocking the
+// host.
+#include <algorithm>
+#include <map>
+
+#include "aegkv_internal.h"
+
+namespace aegkv {
+
+int check_ids_in_range(const int64_t* ids, int64_t n, uint64_t n_pool) {
+  for (int64_t i = 0; i < n; ++i)
+    if (ids[i] < 0 || (uint64_t)ids[i] >= n_pool) return AEGKV_ERR_OUT_OF_RANGE;
+  return AEGKV_OK;
+}
+
+int check_unique(const int64_t* ids, int64_t n) {
+  std::vector<int64_t> v(ids, ids + n);
+  std::sort(v.begin(), v.end());
+  for (size_t i = 1; i < v.size(); ++i)
+    if (v[i] == v[i - 1]) return AEGKV_ERR_DUPLICATE;
+  return AEGKV_OK;
+}
+
+int check_disjoint(const int64_t* a, int64_t na, const int64_t* b, int64_t nb) {
+  std::vector<int64_t> x(a, a + na), y(b, b + nb);
+  std::sort(x.begin(), x.end());
+  std::sort(y.begin(), y.end());
+  size_t i = 0, j = 0;
+  while (i < x.size() && j < y.size()) {
+    if (x[i] == y[j]) return AEGKV_ERR_OVERLAP;
+    if (x[i] < y[j]) ++i; else ++j;
+  }
+  return AEGKV_OK;
+}
+
+namespace {
+std::mutex g_states_mu;
+std::map<int, DeviceState*> g_states;  // one per device, lives until exit
+
+void release_span(DeviceState* ds, const DeviceState::Span& s) {
+  ds->spare_events.push_back(s.ev);
+}
+
+int wait_all(DeviceState* ds) {
+  while (!ds->inflight.empty()) {
+    DeviceState::Span s = ds->inflight.front();
+    ds->inflight.pop_front();
+    hipError_t e = hipEventSynchronize(s.ev);
+    release_span(ds, s);
+    if (e != hipSuccess) return (int)e;
+  }
+  return AEGKV_OK;
+}
+}  // namespace
+
+int current_device_state(DeviceState** out) {
+  int dev = 0;
+  AEGKV_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_states_mu);
+  auto it = g_states.find(dev);
+  if (it != g_states.end()) {
+    *out = it->second;
+    return AEGKV_OK;
+  }
+  auto* ds = new DeviceState();
+  ds->device = dev;
+  hipError_t e = hipDeviceGetAttribute(&ds->num_cu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) {
+    delete ds;
+    return (int)e;
+  }
+  g_states[dev] = ds;
+  *out = ds;
+  return AEGKV_OK;
+}
+
+int ring_acquire(DeviceState* ds, size_t n, size_t* begin) {
+  if (n > ds->cap) {
+    // Grow: every slice of the old ring must be idle before it is freed.
+    int rc = wait_all(ds);
+    if (rc) return rc;
+    if (ds->host_ring) AEGKV_HIP_TRY(hipHostFree(ds->host_ring));
+    if (ds->dev_ring) AEGKV_HIP_TRY(hipFree(ds->dev_ring));
+    ds->host_ring = nullptr;
+    ds->dev_ring = nullptr;
+    size_t cap = std::max<size_t>({n, 2 * ds->cap, (size_t)1 << 17});
+    AEGKV_HIP_TRY(hipHostMalloc((void**)&ds->host_ring, cap * sizeof(int64_t), hipHostMallocDefault));
+    AEGKV_HIP_TRY(hipMalloc((void**)&ds->dev_ring, cap * sizeof(int64_t)));
+    ds->cap = cap;
+    ds->head = 0;
+  }
+  if (ds->head + n > ds->cap) ds->head = 0;
+  size_t b = ds->head, e = b + n;
+  // Wait for in-flight slices that overlap [b, e); drop finished ones.
+  for (auto it = ds->inflight.begin(); it != ds->inflight.end();) {
+    bool overlap = it->begin < e && b < it->end;
+    if (overlap) {
+      hipError_t err = hipEventSynchronize(it->ev);
+      release_span(ds, *it);
+      it = ds->inflight.erase(it);
+      if (err != hipSuccess) return (int)err;
+    } else if (hipEventQuery(it->ev) == hipSuccess) {
+      release_span(ds, *it);
+      it = ds->inflight.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  ds->head = e;
+  *begin = b;
+  return AEGKV_OK;
+}
+
+int ring_commit(DeviceState* ds, hipStream_t stream, size_t begin, size_t n) {
+  hipEvent_t ev;
+  if (!ds->spare_events.empty()) {
+    ev = ds->spare_events.back();
+    ds->spare_events.pop_back();
+  } else {
+    AEGKV_HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  }
+  hipError_t e = hipEventRecord(ev, stream);
+  if (e != hipSuccess) {
+    ds->spare_events.push_back(ev);
+    // The slice may still be read by the enqueued work: wait for the stream.
+    hipStreamSynchronize(stream);
+    return (int)e;
+  }
+  ds->inflight.push_back({begin, begin + n, ev});
+  return AEGKV_OK;
+}
+
+}  // namespace aegkv
+
+extern "C" {
+
+const char* aegkv_strerror(int code) {
+  switch (code) {
+    case AEGKV_OK: return "aegkv: success";
+    case AEGKV_ERR_INVALID_ARG: return "aegkv: invalid argument (null pointer, negative count or zero size)";
+    case AEGKV_ERR_OUT_OF_RANGE: return "aegkv: block id out of range for its pool";
+    case AEGKV_ERR_MISALIGNED: return "aegkv: pointer, stride or size is not 16-byte aligned";
+    case AEGKV_ERR_OVERLAP: return "aegkv: source and destination block sets overlap";
+    case AEGKV_ERR_DUPLICATE: return "aegkv: duplicate destination block id";
+    case AEGKV_ERR_UNSUPPORTED: return "aegkv: unsupported shape or dtype";
+    case AEGKV_ERR_WORKSPACE: return "aegkv: workspace or staging buffer too small";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString((hipError_t)code);
+  return "aegkv: unknown status code";
+}
+
+int aegkv_version(void) { return (1 << 16) | 0; }
+
+int aegkv_init(void) {
+  aegkv::DeviceState* ds = nullptr;
+  int rc = aegkv::current_device_state(&ds);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(ds->mu);
+  if (ds->cap == 0) {
+    size_t b = 0;
+    rc = aegkv::ring_acquire(ds, 1, &b);
+    if (rc) return rc;
+    ds->head = 0;
+  }
+  return AEGKV_OK;
+}
+
+}  // extern "C"

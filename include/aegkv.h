@@ -1,0 +1,196 @@
+/*
+ * aegkv.h — C ABI of the MI355X (gfx950) KV-cache data path for Aegaeon-style
+ * multi-model serving: paged K/V append, block gather/pack/scatter, CPU<->GPU
+ * swap through pinned host memory, block copy/defrag for a multi-shape pool and
+ * paged GQA decode attention.
+ *
+ * Conventions (every entry point):
+ *   - All pointers are borrowed.  Caller-visible memory (pools, staging,
+ *     workspaces, outputs) is owned by the caller; the library never frees it.
+ *     The library keeps one private, per-device upload ring for host id lists
+ *     (pinned host + device memory, grown on demand and reused).
+ *   - Work is enqueued asynchronously on the explicit `stream` (a hipStream_t;
+ *     NULL = the legacy default stream).  Functions return after enqueueing.
+ *   - Return value: 0 = success; < 0 = invalid argument (AEGKV_ERR_*), detected
+ *     on the host before anything is enqueued; > 0 = a hipError_t returned by the
+ *     HIP runtime.  aegkv_strerror() names every code.  No C++ exception crosses
+ *     the ABI.
+ *   - Sizes are in bytes unless the name says "elements"; element strides are in
+ *     elements of the K/V dtype.
+ *   - Block ids in host arrays are int64 (the reference passes
+ *     std::vector<int64_t>); block tables and sequence lengths on the device are
+ *     int32 and slot mappings are int64, as in the vLLM attention metadata the
+ *     reference builds.
+ *
+ * Reference interfaces each entry point replaces are cited as path:line relative
+ * to the Zyyeric/Aegaeon repository.  Entries marked EXT replace vLLM 0.5.1 /
+ * vllm-flash-attn kernels that the reference reaches through the model forward
+ * (aegaeon/aegaeon/worker.py:517-523).
+ */
+#ifndef AEGKV_H
+#define AEGKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* aegkv_stream_t; /* hipStream_t */
+
+/* ---- status codes ------------------------------------------------------ */
+#define AEGKV_OK 0
+#define AEGKV_ERR_INVALID_ARG (-1)   /* null pointer, negative count, zero size  */
+#define AEGKV_ERR_OUT_OF_RANGE (-2)  /* a block id outside its pool             */
+#define AEGKV_ERR_MISALIGNED (-3)    /* pointer/stride/size not 16-byte aligned  */
+#define AEGKV_ERR_OVERLAP (-4)       /* src and dst block sets share a block     */
+#define AEGKV_ERR_DUPLICATE (-5)     /* a destination block id appears twice     */
+#define AEGKV_ERR_UNSUPPORTED (-6)   /* shape/dtype the kernels do not cover     */
+#define AEGKV_ERR_WORKSPACE (-7)     /* workspace/staging smaller than required  */
+
+/* dtype codes for the K/V and query elements */
+#define AEGKV_DTYPE_BF16 0
+#define AEGKV_DTYPE_FP16 1
+
+/* Human-readable name of a status code (static storage, never NULL). */
+const char* aegkv_strerror(int code);
+
+/* Library ABI version: (major << 16) | minor. */
+int aegkv_version(void);
+
+/* Optional per-device set-up for the current device (creates the id upload
+ * ring).  Every entry point does it lazily; calling it early keeps the first
+ * real call free of set-up cost. */
+int aegkv_init(void);
+
+/* ---- a1: CPU<->GPU block swap ------------------------------------------
+ * Replaces aegaeon.ops.swap (aegaeon/ops/ops.h:4-10, aegaeon/ops/swap.cu:25-59,
+ * bound at aegaeon/ops/ops.cpp:4-5, called at aegaeon/aegaeon/worker.py:756-762).
+ * For i in [0, n): the block `src_ids[i]` of the source pool is copied byte for
+ * byte to block `dst_ids[i]` of the destination pool.  is_swap_in != 0 copies
+ * host -> device (source = host_pool), otherwise device -> host.  Block i of a
+ * pool starts at base + i*block_bytes (swap.cu:43-44,52-53).
+ *   src_ids/dst_ids: HOST arrays of n int64 ids (like the reference's vectors).
+ *   host_pool: pinned host memory (hipHostMalloc / torch pin_memory).
+ *   staging/staging_bytes: optional device buffer.  With staging, scattered device
+ *     blocks are packed by a gfx950 kernel into staging and moved with one DMA per
+ *     run of consecutive host ids; without it (staging == NULL), one DMA per run of
+ *     consecutive (src, dst) pairs.  The result is identical.
+ * Unlike the reference, ids are range-checked and duplicate destination ids are
+ * rejected (AEGKV_ERR_DUPLICATE) before anything is enqueued. */
+int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+                      int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
+                      void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
+                      void* staging, uint64_t staging_bytes, aegkv_stream_t stream);
+
+/* ---- block gather / scatter / copy / defrag ----------------------------
+ * Device-to-device block copies driven by HOST id lists (the lists the block
+ * manager builds in move_requests, aegaeon/aegaeon/block_manager.py:822-832).
+ * copy:    dst_pool[dst_ids[i]] <- src_pool[src_ids[i]]; a NULL id array means the
+ *          identity (i), so NULL dst_ids packs and NULL src_ids scatters.  When the
+ *          two pools are the same memory, src and dst sets must be disjoint
+ *          (AEGKV_ERR_OVERLAP) so that one parallel kernel is exact.
+ * pack:    staging[i] <- pool[ids[i]]        (swap-out gather, block-table driven)
+ * scatter: pool[ids[i]] <- staging[i]        (swap-in scatter)
+ * defrag:  pool[dst_ids[i]] <- pool[src_ids[i]] with disjoint src/dst (a10: the
+ *          reference has no KV compaction; the nearest precedent is
+ *          aegaeon/aegaeon/loader/allocator.py:288-321).
+ * block_bytes must be a multiple of 16 and pool bases 16-byte aligned. */
+int aegkv_copy_blocks(const void* src_pool, uint64_t n_src_blocks, void* dst_pool,
+                      uint64_t n_dst_blocks, const int64_t* src_ids,
+                      const int64_t* dst_ids, int64_t n, uint64_t block_bytes,
+                      aegkv_stream_t stream);
+int aegkv_pack_blocks(const void* pool, uint64_t n_pool_blocks, const int64_t* ids,
+                      int64_t n, void* staging, uint64_t block_bytes,
+                      aegkv_stream_t stream);
+int aegkv_scatter_blocks(const void* staging, const int64_t* ids, int64_t n,
+                         void* pool, uint64_t n_pool_blocks, uint64_t block_bytes,
+                         aegkv_stream_t stream);
+int aegkv_defrag_blocks(void* pool, uint64_t n_pool_blocks, const int64_t* src_ids,
+                        const int64_t* dst_ids, int64_t n, uint64_t block_bytes,
+                        aegkv_stream_t stream);
+
+/* ---- a5: slot-mapped K/V append (EXT reshape_and_cache_flash) -----------
+ * For layer l in [0, n_layers) and token t in [0, n_tokens) with
+ * s = slot_mapping[t] in [0, n_blocks*block_size):
+ *   key_cache  + l*cache_layer_stride + (s/block_size)*cache_block_stride
+ *              + (s%block_size)*row  <-  key   + l*key_layer_stride   + t*key_token_stride
+ *   value_cache likewise from value, with row = n_kv_heads*head_dim elements.
+ * Slots < 0 (vLLM padding) and slots >= n_blocks*block_size are skipped.  The
+ * slot mapping is the reference's slot = block_table[pos/16]*16 + pos%16
+ * (aegaeon/aegaeon/worker.py:628-633).  With the reference's storage layout
+ * [N, L, 2, 16, Hkv, D] (worker.py:389-395) one call appends every layer:
+ * cache_block_stride = L*2*16*Hkv*D, cache_layer_stride = 2*16*Hkv*D and
+ * value_cache = key_cache + 16*Hkv*D.  n_layers = 1 is the per-layer vLLM call.
+ * slot_mapping is a DEVICE int64 array; element size is elem_bytes (2). */
+int aegkv_kv_append(const void* key, const void* value, int64_t key_token_stride,
+                    int64_t value_token_stride, int64_t key_layer_stride,
+                    int64_t value_layer_stride, const int64_t* slot_mapping,
+                    int64_t n_tokens, void* key_cache, void* value_cache,
+                    int64_t cache_block_stride, int64_t cache_layer_stride,
+                    int64_t n_blocks, int32_t n_layers, int32_t block_size,
+                    int32_t n_kv_heads, int32_t head_dim, int32_t elem_bytes,
+                    aegkv_stream_t stream);
+
+/* ---- gather_tokens: block-table de-page ----------------------------------
+ * For sequence b, token p < seq_lens[b] and layer l < n_layers:
+ *   out_key[l*out_layer_stride + (cu_seqlens[b]+p)*row] <-
+ *       key_cache[l*cache_layer_stride + block_tables[b][p/bs]*cache_block_stride
+ *                 + (p%bs)*row]
+ * and out_value likewise.  block_tables [batch][max_blocks] int32, seq_lens [batch]
+ * int32 and cu_seqlens [batch+1] int32 are DEVICE arrays; max_seq_len is a host
+ * upper bound of seq_lens that sizes the grid (longer device lengths are clamped
+ * to it); out_tokens is the output capacity in tokens per layer, and tokens that
+ * would land past it are not written.  Pad entries of the block table
+ * (id 0 in the reference, worker.py:640-646) past ceil(len/bs) are never read;
+ * a block id outside [0, n_blocks) is never dereferenced (its tokens are left
+ * unwritten in the output). */
+int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
+                        int64_t cache_block_stride, int64_t cache_layer_stride,
+                        int64_t n_blocks, const int32_t* block_tables, int32_t max_blocks,
+                        const int32_t* seq_lens, const int32_t* cu_seqlens,
+                        int32_t batch, int32_t max_seq_len, void* out_key,
+                        void* out_value, int64_t out_tokens, int64_t out_layer_stride,
+                        int32_t n_layers,
+                        int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
+                        int32_t elem_bytes, aegkv_stream_t stream);
+
+/* ---- a6: paged GQA decode attention (EXT flash_attn_with_kvcache) --------
+ * out[b][h][:] = sum_{j < seq_lens[b]} softmax_j(scale * q[b][h] . K_j) V_j with
+ * K_j/V_j the kv head h / (n_q_heads/n_kv_heads) of token j read through
+ * block_tables[b][j/block_size] (selected at aegaeon/aegaeon/worker.py:410-418,
+ * metadata at worker.py:694-711).  fp32 accumulation, dtype I/O.
+ *   q/out: [batch][n_q_heads][head_dim], batch strides in elements.
+ *   key_cache/value_cache: [N][block_size][n_kv_heads][head_dim] per block with
+ *     block stride cache_block_stride (the reference's permuted per-layer view).
+ *   block_tables [batch][max_blocks] int32, seq_lens [batch] int32: DEVICE arrays.
+ *   max_seq_len: host upper bound of seq_lens (sizes the split-KV grid); device
+ *     lengths above it are clamped to it, so a wrong bound never reads or writes
+ *     out of bounds.
+ *   blocks_per_split: KV blocks per work item (0 = library default).
+ *   workspace: DEVICE scratch for split-KV partials of
+ *     aegkv_paged_decode_attention_workspace_size(...) bytes.
+ * Supported: block_size 16, head_dim 64/128/256, n_q_heads/n_kv_heads <= 16.
+ * seq_lens[b] == 0 yields zeros.  A block id outside [0, n_blocks) is never
+ * dereferenced: its tokens are masked out of the softmax. */
+int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_heads,
+                                                     int32_t head_dim,
+                                                     int32_t max_seq_len,
+                                                     int32_t block_size,
+                                                     int32_t blocks_per_split);
+int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void* q,
+                                 int64_t q_batch_stride, const void* key_cache,
+                                 const void* value_cache, int64_t cache_block_stride,
+                                 int64_t n_blocks, const int32_t* block_tables,
+                                 int32_t max_blocks, const int32_t* seq_lens,
+                                 int32_t batch, int32_t max_seq_len, int32_t n_q_heads,
+                                 int32_t n_kv_heads, int32_t head_dim,
+                                 int32_t block_size, float scale, int32_t dtype,
+                                 int32_t blocks_per_split, void* workspace,
+                                 uint64_t workspace_bytes, aegkv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AEGKV_H */

@@ -1,0 +1,121 @@
+"""GPU parity of the slot-mapped append (vLLM reshape_and_cache_flash semantics,
+reached from aegaeon/aegaeon/worker.py:517-523) and the block-table gather."""
+import numpy as np
+import pytest
+import torch
+
+from aegaeon_amd import attention as A
+from aegaeon_amd.workloads import QWEN25_7B, qwen_append_batch
+from oracle import kv_oracle as ko
+from tests.kvtest_utils import load_golden, random_bits, to_bits, to_device_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def test_golden_append_then_gather(device):
+    z = load_golden()
+    N, L, H, D, BS = (int(x) for x in z["geometry"])
+    cache = to_device_bits(z["pool"], "fp16", device).view(N, L, 2, BS, H, D)
+    key = to_device_bits(z["new_k"], "fp16", device).view(1, -1, H, D)
+    val = to_device_bits(z["new_v"], "fp16", device).view(1, -1, H, D)
+    slots = torch.from_numpy(z["slots"]).to(device)
+    A.append_kv(key, val, cache, slots)
+    expect = z["pool"].copy()
+    expect[z["append_idx"]] = z["append_val"]
+    assert np.array_equal(to_bits(cache).reshape(-1), expect)
+    sl = z["seq_lens"]
+    bt = torch.from_numpy(z["tables"]).to(device)
+    out_k, out_v = A.gather_tokens(cache, bt, torch.from_numpy(sl.astype(np.int32)).to(device),
+                                   int(sl.sum()), int(sl.max()))
+    assert np.array_equal(to_bits(out_k)[0], z["out_k"])
+    assert np.array_equal(to_bits(out_v)[0], z["out_v"])
+
+
+def test_per_layer_reshape_and_cache_flash(device):
+    """vLLM's per-layer call through the permuted view (worker.py:419-451)
+    equals the oracle, including padding slots (-1) and strided keys."""
+    rng = np.random.default_rng(11)
+    N, L, H, D = 40, 3, 4, 128
+    bits = random_bits(rng, (N, L, 2, 16, H, D), "bf16")
+    cache = to_device_bits(bits, "bf16", device)
+    view = cache.permute(1, 2, 0, 3, 4, 5)
+    T = 37
+    qkv = to_device_bits(random_bits(rng, (T, 3 * H * D), "bf16"), "bf16", device)
+    key = qkv[:, H * D:2 * H * D].view(T, H, D)      # token stride 3*H*D
+    val = qkv[:, 2 * H * D:].view(T, H, D)
+    slots_np = rng.permutation(N * 16)[:T].astype(np.int64)
+    slots_np[[3, 20]] = -1
+    slots = torch.from_numpy(slots_np).to(device)
+    ref = bits.copy()
+    rview = ref.transpose(1, 2, 0, 3, 4, 5)
+    kb, vb = to_bits(key), to_bits(val)
+    for layer in range(L):
+        A.reshape_and_cache_flash(key, val, view[layer, 0], view[layer, 1], slots)
+        ko.reshape_and_cache_flash(kb, vb, rview[layer, 0], rview[layer, 1], slots_np)
+    assert np.array_equal(to_bits(cache), ref)
+
+
+def test_out_of_range_slots_skipped(device):
+    """Slots < 0 and >= N*16 never write; every other byte is untouched."""
+    rng = np.random.default_rng(5)
+    N, L, H, D = 8, 2, 2, 64
+    cache = torch.full((N, L, 2, 16, H, D), float("nan"), dtype=torch.float16, device=device)
+    before = to_bits(cache)
+    key = to_device_bits(random_bits(rng, (L, 4, H, D), "fp16"), "fp16", device)
+    val = to_device_bits(random_bits(rng, (L, 4, H, D), "fp16"), "fp16", device)
+    slots_np = np.asarray([-1, N * 16, 5, N * 16 + 100], dtype=np.int64)
+    A.append_kv(key, val, cache, torch.from_numpy(slots_np).to(device))
+    got = to_bits(cache)
+    ref = before.copy()
+    ko.append_layers(to_bits(key), to_bits(val), ref, np.asarray([-1, -1, 5, -1]))
+    assert np.array_equal(got, ref)
+
+
+def test_qwen_full_size_append(device):
+    """Qwen2.5-7B shape, 256 sequences, pool = 2x need (17.4 GB): each appended
+    row reads back exactly (append -> gather identity) and no other byte
+    changes (count of modified elements)."""
+    wb = qwen_append_batch(0)
+    g = wb.geometry
+    N = wb.n_pool_blocks
+    cache = torch.empty((N, *g.block_shape), dtype=torch.bfloat16, device=device)
+    cache.view(torch.int16).fill_(0x7FC1)  # a NaN pattern the inputs never hold
+    gen = torch.Generator(device=device).manual_seed(0)
+    key = torch.randn((g.n_layers, wb.batch, g.n_kv_heads, g.head_dim), generator=gen,
+                      device=device).to(torch.bfloat16)
+    val = torch.randn(key.shape, generator=gen, device=device).to(torch.bfloat16)
+    slots_np = wb.slot_mapping()
+    slots = torch.from_numpy(slots_np).to(device)
+    A.append_kv(key, val, cache, slots)
+    blk = slots // 16
+    off = slots % 16
+    got_k = cache[blk, :, 0, off]  # [B, L, H, D]
+    got_v = cache[blk, :, 1, off]
+    assert torch.equal(got_k.view(torch.int16), key.transpose(0, 1).view(torch.int16))
+    assert torch.equal(got_v.view(torch.int16), val.transpose(0, 1).view(torch.int16))
+    changed = int((cache.view(torch.int16) != 0x7FC1).sum())
+    inputs_hit_pattern = int((key.view(torch.int16) == 0x7FC1).sum() + (val.view(torch.int16) == 0x7FC1).sum())
+    assert changed + inputs_hit_pattern == 2 * key.numel()
+
+
+def test_gather_qwen_layers_subset(device):
+    """gather of layers (5, 3) of a Qwen-shaped pool equals the oracle."""
+    rng = np.random.default_rng(9)
+    g = QWEN25_7B
+    N = 64
+    bits = random_bits(rng, (N, *g.block_shape), "bf16")
+    cache = to_device_bits(bits, "bf16", device)
+    lens = np.asarray([1, 15, 16, 17, 100, 0, 33], dtype=np.int64)
+    need = [-(-int(x) // 16) for x in lens]
+    ids = rng.permutation(N)[:sum(need)]
+    tables, o = [], 0
+    for c in need:
+        tables.append([int(x) for x in ids[o:o + c]])
+        o += c
+    padded = ko.pad_block_tables(tables)
+    bt = torch.from_numpy(padded).to(device)
+    out_k, out_v = A.gather_tokens(cache, bt, torch.from_numpy(lens.astype(np.int32)).to(device),
+                                   int(lens.sum()), int(lens.max()), layers=(5, 3))
+    rk, rv = ko.gather_tokens(bits, tables, lens, layers=[5, 6, 7])
+    assert np.array_equal(to_bits(out_k), rk)
+    assert np.array_equal(to_bits(out_v), rv)
