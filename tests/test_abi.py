@@ -1,0 +1,141 @@
+"""The C ABI without a GPU: libaegkv.so loads, exports every function that
+include/aegkv.h declares, and rejects bad arguments on the host with the
+documented status codes before any HIP call is made (pointers here are host
+addresses that the library never dereferences on these paths)."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from aegaeon_amd import _lib
+
+OK, INVALID, RANGE, MISALIGNED, OVERLAP, DUP, UNSUP, WS = 0, -1, -2, -3, -4, -5, -6, -7
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def _i64(a):
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.int64))
+    return a, a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+
+
+def _buf(nbytes, misalign=0):
+    raw = np.zeros(nbytes + 64, dtype=np.uint8)
+    base = raw.ctypes.data
+    addr = (base + 15) // 16 * 16 + misalign
+    return raw, addr
+
+
+def test_every_declared_symbol_is_exported_and_typed(lib):
+    declared = _lib.declared_symbols()
+    assert len(declared) >= 12
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_header_status_codes_match_strerror(lib):
+    text = _lib.HEADER_PATH.read_text()
+    codes = {m[0]: int(m[1]) for m in re.findall(r"#define (AEGKV_(?:OK|ERR_\w+)) \(?(-?\d+)\)?", text)}
+    assert codes["AEGKV_OK"] == OK and codes["AEGKV_ERR_WORKSPACE"] == WS
+    msgs = {c: _lib.strerror(c) for c in codes.values()}
+    assert len(set(msgs.values())) == len(msgs)  # every code has its own message
+    assert "unknown" in _lib.strerror(-99)
+    assert lib.aegkv_version() >> 16 == 1
+
+
+def test_block_copy_argument_checks(lib):
+    raw, pool = _buf(16 * 64)
+    s, sp = _i64([0, 1, 2])
+    d, dp = _i64([3, 4, 5])
+    bad, badp = _i64([0, 64, 1])
+    dup, dupp = _i64([6, 6, 7])
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, dp, -1, 16, None) == INVALID
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, dp, 0, 16, None) == OK  # no-op
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, badp, dp, 3, 16, None) == RANGE
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, badp, 3, 16, None) == RANGE
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, dupp, 3, 16, None) == DUP
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, sp, 3, 16, None) == OVERLAP
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, dp, 3, 24, None) == MISALIGNED
+    raw2, mis = _buf(16 * 64, misalign=8)
+    assert lib.aegkv_copy_blocks(mis, 64, pool, 64, sp, dp, 3, 16, None) == MISALIGNED
+    # partially aliased distinct pools would make the order matter
+    assert lib.aegkv_copy_blocks(pool, 64, pool + 16, 63, sp, dp, 3, 16, None) == OVERLAP
+    assert lib.aegkv_defrag_blocks(pool, 64, sp, sp, 3, 16, None) == OVERLAP
+    assert lib.aegkv_defrag_blocks(pool, 64, None, dp, 3, 16, None) == INVALID
+    assert lib.aegkv_pack_blocks(pool, 64, None, 3, pool, 16, None) == INVALID
+    assert lib.aegkv_scatter_blocks(pool, badp, 3, pool, 64, 16, None) == RANGE
+
+
+def test_swap_argument_checks(lib):
+    raw, dev = _buf(16 * 8)
+    host = np.zeros(16 * 8, dtype=np.uint8)
+    s, sp = _i64([0, 1])
+    big, bigp = _i64([0, 8])
+    dup, dupp = _i64([2, 2])
+    h = host.ctypes.data
+    assert lib.aegkv_swap_blocks(sp, sp, -1, 0, dev, 8, h, 8, 16, None, 0, None) == INVALID
+    assert lib.aegkv_swap_blocks(sp, sp, 0, 0, dev, 8, h, 8, 16, None, 0, None) == OK
+    assert lib.aegkv_swap_blocks(None, sp, 2, 0, dev, 8, h, 8, 16, None, 0, None) == INVALID
+    assert lib.aegkv_swap_blocks(bigp, sp, 2, 0, dev, 8, h, 8, 16, None, 0, None) == RANGE
+    assert lib.aegkv_swap_blocks(sp, bigp, 2, 1, dev, 8, h, 8, 16, None, 0, None) == RANGE
+    assert lib.aegkv_swap_blocks(sp, dupp, 2, 0, dev, 8, h, 8, 16, None, 0, None) == DUP
+    assert lib.aegkv_swap_blocks(sp, sp, 2, 0, dev, 8, h, 8, 0, None, 0, None) == INVALID
+
+
+def test_append_and_gather_argument_checks(lib):
+    raw, p = _buf(4096)
+    raw2, mis = _buf(4096, misalign=2)
+    args = dict(n_tokens=4, n_layers=1, bs=16, H=2, D=64, eb=2)
+
+    def append(key=p, elem=2, tok_stride=128, n_layers=1, n_tokens=4, heads=2, dim=64):
+        return lib.aegkv_kv_append(key, p, tok_stride, 128, 0, 0, p, n_tokens, p, p, 4096, 0, 4,
+                                   n_layers, 16, heads, dim, elem, None)
+
+    assert append(elem=4) == UNSUP
+    assert append(n_layers=0) == INVALID
+    assert append(n_tokens=0) == OK
+    assert append(key=mis) == MISALIGNED
+    assert append(tok_stride=3) == MISALIGNED
+    assert append(dim=3) == MISALIGNED  # 2*3*2 = 12-byte rows
+    # gather: max_seq_len needs more blocks than the table is wide
+    assert lib.aegkv_gather_tokens(p, p, 4096, 0, 4, p, 1, p, p, 2, 40, p, p, 80, 0, 1, 16, 2,
+                                   64, 2, None) == INVALID
+    assert lib.aegkv_gather_tokens(p, p, 4096, 0, 4, p, 3, p, p, 2, 40, p, p, 80, 0, 1, 16, 2,
+                                   64, 4, None) == UNSUP
+    assert lib.aegkv_gather_tokens(p, p, 4096, 0, 4, p, 3, p, p, 0, 40, p, p, 80, 0, 1, 16, 2,
+                                   64, 2, None) == OK
+    del args
+
+
+def test_attention_argument_checks_and_workspace_size(lib):
+    raw, p = _buf(1 << 16)
+    ws = lib.aegkv_paged_decode_attention_workspace_size
+    assert ws(4, 28, 128, 0, 16, 0) == 0
+    assert ws(4, 28, 128, 100, 12, 0) == INVALID
+    big = ws(128, 28, 128, 8192, 16, 0)
+    assert big > 0 and big == ws(128, 28, 128, 8192, 16, 0)
+    assert ws(128, 28, 128, 8192, 16, 0) >= ws(128, 28, 128, 4096, 16, 0)
+
+    def attn(Hq=28, Hkv=4, D=128, bs=16, dtype=0, max_len=64, max_blocks=4, wsp=None, wsb=0,
+             bps=0, q=p):
+        return lib.aegkv_paged_decode_attention(p, Hq * D, q, Hq * D, p, p, 16 * Hkv * D, 8, p,
+                                                max_blocks, p, 2, max_len, Hq, Hkv, D, bs, 0.1,
+                                                dtype, bps, wsp, wsb, None)
+
+    assert attn(Hq=30) == INVALID
+    assert attn(D=96) == UNSUP
+    assert attn(bs=32) == UNSUP
+    assert attn(dtype=7) == UNSUP
+    assert attn(Hq=34, Hkv=2) == UNSUP  # group of 17 > 16
+    assert attn(max_len=100) == INVALID  # needs 7 blocks, table has 4
+    need = ws(2, 28, 128, 4096, 16, 1)
+    assert need > 0
+    assert attn(max_len=4096, max_blocks=256, bps=1) == WS
+    assert attn(max_len=4096, max_blocks=256, bps=1, wsp=p, wsb=need - 1) == WS
+    raw2, mis = _buf(64, misalign=4)
+    assert attn(q=mis) == MISALIGNED

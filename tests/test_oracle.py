@@ -1,0 +1,237 @@
+"""Pins of the CPU oracle (runs without a GPU).
+
+Each check fixes an oracle function by something other than the oracle's own
+formula: the golden fixture written by per-element flat-index loops
+(tests/golden/make_golden.py), hand-computed literals, torch's float64
+scaled_dot_product_attention, closed forms of softmax attention, torch's own
+bf16/fp16 rounding, and brute force on tiny inputs.  A plausible slip in the
+oracle (a transposed view, h % G instead of h // G for GQA, an off-by-one in
+the slot formula, a dropped max-subtraction) fails at least one of them.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as ko
+from tests.kvtest_utils import load_golden, random_bits
+
+
+# ---------------------------------------------------------------- golden fixture
+def test_golden_slots_match_oracle_slot_mapping():
+    z = load_golden()
+    ctx = z["context_lens"]
+    nb = [-(-int(c + 1) // 16) for c in ctx]
+    tables = [list(map(int, z["tables"][i, :nb[i]])) for i in range(len(ctx))]
+    got = ko.slot_mapping(tables, ctx, ctx + 1)
+    assert np.array_equal(got, z["slots"])
+
+
+def test_golden_append_matches_oracle():
+    z = load_golden()
+    N, L, H, D, BS = (int(x) for x in z["geometry"])
+    pool = z["pool"].copy().reshape(N, L, 2, BS, H, D)
+    ko.append_layers(z["new_k"].reshape(1, -1, H, D), z["new_v"].reshape(1, -1, H, D), pool,
+                     z["slots"])
+    expect = z["pool"].copy()
+    expect[z["append_idx"]] = z["append_val"]
+    assert np.array_equal(pool.reshape(-1), expect)
+
+
+def test_golden_gather_matches_oracle():
+    z = load_golden()
+    N, L, H, D, BS = (int(x) for x in z["geometry"])
+    pool = z["pool"].copy()
+    pool[z["append_idx"]] = z["append_val"]
+    sl = z["seq_lens"]
+    tables = [list(map(int, z["tables"][i, :-(-int(ln) // BS)])) for i, ln in enumerate(sl)]
+    ok_, ov = ko.gather_tokens(pool.reshape(N, L, 2, BS, H, D), tables, sl)
+    assert np.array_equal(ok_[0], z["out_k"])
+    assert np.array_equal(ov[0], z["out_v"])
+
+
+def test_golden_swap_matches_oracle():
+    z = load_golden()
+    N, L, H, D, BS = (int(x) for x in z["geometry"])
+    pool = z["pool"].copy()
+    pool[z["append_idx"]] = z["append_val"]
+    n = len(z["swap_src"])
+    host = np.zeros((n, L, 2, BS, H, D), dtype=np.uint16)
+    ko.swap_blocks(z["swap_src"], z["swap_dst"], False, pool.reshape(N, L, 2, BS, H, D), host)
+    assert np.array_equal(host.reshape(-1), z["host_after_swap"])
+
+
+# ---------------------------------------------------------------- literals
+def test_slot_mapping_literals():
+    bt = [[7, 3, 9]]
+    # positions 0, 15, 16, 17, 33 of one sequence (context 0, seq_len 34)
+    got = ko.slot_mapping(bt, [0], [34])
+    assert got[0] == 112 and got[15] == 127 and got[16] == 48 and got[17] == 49
+    assert got[32] == 144 and got[33] == 145
+    # only the new tokens [context_len, seq_len) are mapped, concatenated over requests
+    got = ko.slot_mapping([[5], [2, 8]], [15, 16], [16, 18])
+    assert got.tolist() == [95, 128, 129]
+    assert ko.slot_mapping([[4]], [0], [1]).tolist() == [64]  # length 1
+
+
+def test_pad_block_tables_literal():
+    out = ko.pad_block_tables([[3, 1], [], [9, 8, 7]])
+    assert out.dtype == np.int32
+    assert out.tolist() == [[3, 1, 0], [0, 0, 0], [9, 8, 7]]
+
+
+def test_append_literal_index():
+    """storage [N, L, 2, 16, H, D]: layer l's key row of slot s sits at
+    flat ((((s//16)*L + l)*2 + 0)*16 + s%16)*H*D."""
+    N, L, H, D = 5, 3, 2, 4
+    st = np.zeros((N, L, 2, 16, H, D), dtype=np.int64)
+    key = np.arange(L * 2 * H * D).reshape(L, 2, H, D) + 1
+    val = -key
+    ko.append_layers(key, val, st, np.asarray([37, -1]))
+    flat = st.reshape(-1)
+    for l in range(L):
+        kb = ((((37 // 16) * L + l) * 2 + 0) * 16 + 37 % 16) * H * D
+        vb = ((((37 // 16) * L + l) * 2 + 1) * 16 + 37 % 16) * H * D
+        assert np.array_equal(flat[kb:kb + H * D], key[l, 0].reshape(-1))
+        assert np.array_equal(flat[vb:vb + H * D], val[l, 0].reshape(-1))
+    assert np.count_nonzero(flat) == 2 * L * H * D  # slot -1 wrote nothing
+
+
+def test_brute_force_pack_scatter_copy():
+    rng = np.random.default_rng(0)
+    pool = rng.integers(0, 256, size=(9, 24), dtype=np.uint8)
+    ids = [4, 0, 7]
+    st = ko.pack_blocks(pool, ids)
+    for i, b in enumerate(ids):
+        for j in range(24):
+            assert st[i, j] == pool[b, j]
+    other = np.zeros_like(pool)
+    ko.scatter_blocks(st, [8, 1, 2], other)
+    assert np.array_equal(other[[8, 1, 2]], pool[ids]) and not other[[0, 3, 4, 5, 6, 7]].any()
+    third = np.zeros_like(pool)
+    ko.copy_blocks(pool, third, None, [5, 6])
+    assert np.array_equal(third[5], pool[0]) and np.array_equal(third[6], pool[1])
+
+
+def test_swap_later_pair_wins_on_duplicate_destination():
+    """The reference issues its copies in list order on one stream
+    (aegaeon/ops/swap.cu:36-58), so a repeated destination keeps the last."""
+    cache = np.arange(4 * 2).reshape(4, 2).astype(np.uint16)
+    host = np.zeros((2, 2), dtype=np.uint16)
+    ko.swap_blocks([1, 3], [0, 0], False, cache, host)
+    assert host[0].tolist() == cache[3].tolist()
+
+
+# ---------------------------------------------------------------- dtype rounding
+@pytest.mark.parametrize("dtype,tdt", [("bf16", torch.bfloat16), ("fp16", torch.float16)])
+def test_bit_conversions_match_torch(dtype, tdt):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(4000) * 10.0 ** rng.integers(-6, 5, 4000),
+                        [0.0, -0.0, 1.0, 65504.0, 1e-8, np.inf, -np.inf]]).astype(np.float32)
+    got = ko.float_to_bits(x, dtype)
+    want = torch.from_numpy(x).to(tdt).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    back = ko.bits_to_float(want, dtype)
+    assert np.array_equal(back, torch.from_numpy(want.view(np.int16)).view(tdt).double().numpy())
+
+
+# ---------------------------------------------------------------- attention
+def _paged_case(rng, lens, Hq, Hkv, D, dtype="bf16"):
+    need = [-(-int(x) // 16) for x in lens]
+    N = 2 * sum(need) + 3
+    ids = rng.permutation(N)[:sum(need)]
+    tables, o = [], 0
+    for c in need:
+        tables.append([int(x) for x in ids[o:o + c]])
+        o += c
+    kc = ko.bits_to_float(random_bits(rng, (N, 16, Hkv, D), dtype), dtype)
+    vc = ko.bits_to_float(random_bits(rng, (N, 16, Hkv, D), dtype), dtype)
+    q = ko.bits_to_float(random_bits(rng, (len(lens), Hq, D), dtype), dtype)
+    return tables, ko.pad_block_tables(tables), q, kc, vc
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(28, 4, 128), (8, 8, 64), (6, 2, 32)])
+def test_attention_matches_torch_sdpa_fp64(Hq, Hkv, D):
+    rng = np.random.default_rng(Hq + D)
+    lens = [1, 16, 17, 40]
+    tables, padded, q, kc, vc = _paged_case(rng, lens, Hq, Hkv, D)
+    scale = 1 / math.sqrt(D)
+    got = ko.paged_decode_attention(q, kc, vc, padded, lens, scale)
+    G = Hq // Hkv
+    for b, ln in enumerate(lens):
+        # gather the sequence by explicit per-token block lookups
+        k = np.stack([kc[tables[b][p // 16], p % 16] for p in range(ln)])  # [T, Hkv, D]
+        v = np.stack([vc[tables[b][p // 16], p % 16] for p in range(ln)])
+        kt = torch.from_numpy(k).permute(1, 0, 2).repeat_interleave(G, dim=0)  # [Hq, T, D]
+        vt = torch.from_numpy(v).permute(1, 0, 2).repeat_interleave(G, dim=0)
+        qt = torch.from_numpy(q[b]).unsqueeze(1)  # [Hq, 1, D]
+        want = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, scale=scale)
+        np.testing.assert_allclose(got[b], want[:, 0].numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(3)
+    Hq, Hkv, D = 8, 2, 16
+    tables, padded, q, kc, vc = _paged_case(rng, [1, 30], Hq, Hkv, D)
+    # len 1: output is V0 of each sequence's kv head, for every query head of the group
+    out = ko.paged_decode_attention(q, kc, vc, padded, [1, 30], 0.125)
+    assert np.array_equal(out[0], np.repeat(vc[tables[0][0], 0], Hq // Hkv, axis=0))
+    # equal keys: uniform softmax -> mean of the values
+    kc2 = kc.copy()
+    kc2[:] = kc[0, 0]
+    out = ko.paged_decode_attention(q, kc2, vc, padded, [1, 30], 0.125)
+    v = np.stack([vc[tables[1][p // 16], p % 16] for p in range(30)]).mean(axis=0)
+    np.testing.assert_allclose(out[1], np.repeat(v, Hq // Hkv, axis=0), rtol=1e-12, atol=1e-12)
+    # a dominant logit selects its value row; large logits must not overflow
+    kc3 = kc.copy() * 0.0
+    kc3[tables[1][1], 3] = 1000.0  # token 19
+    q3 = np.abs(q) + 1.0
+    out = ko.paged_decode_attention(q3, kc3, vc, padded, [1, 30], 1.0)
+    assert np.isfinite(out).all()
+    np.testing.assert_allclose(out[1], np.repeat(vc[tables[1][1], 3], Hq // Hkv, axis=0),
+                               rtol=0, atol=1e-9)
+
+
+def test_attention_gqa_equals_mha_with_repeated_heads():
+    rng = np.random.default_rng(4)
+    tables, padded, q, kc, vc = _paged_case(rng, [23, 5], 6, 2, 32)
+    gqa = ko.paged_decode_attention(q, kc, vc, padded, [23, 5], 0.2)
+    mha = ko.paged_decode_attention(q, np.repeat(kc, 3, axis=2), np.repeat(vc, 3, axis=2),
+                                    padded, [23, 5], 0.2)
+    np.testing.assert_allclose(gqa, mha, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_ignores_padding_and_stale_rows():
+    rng = np.random.default_rng(5)
+    tables, padded, q, kc, vc = _paged_case(rng, [5, 18], 4, 2, 16)
+    ref = ko.paged_decode_attention(q, kc, vc, padded, [5, 18], 0.25)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[tables[0][0], 5:] = np.nan
+    vc2[tables[1][1], 2:] = np.nan
+    wide = np.pad(padded, ((0, 0), (0, 3)))
+    out = ko.paged_decode_attention(q, kc2, vc2, wide, [5, 18], 0.25)
+    assert np.array_equal(out, ref)
+
+
+# ---------------------------------------------------------------- defrag plan
+@pytest.mark.parametrize("seed", range(5))
+def test_defrag_plan_invariants(seed):
+    rng = np.random.default_rng(seed)
+    valid = sorted(rng.permutation(400)[:150].tolist())  # a shape's (sparse) id space
+    live = rng.permutation(valid)[:70].tolist()
+    src, dst = ko.plan_defrag(live, valid)
+    assert not set(src) & set(dst)
+    assert len(set(src)) == len(src) == len(set(dst)) == len(dst)
+    tables = [live[i:i + 7] for i in range(0, 70, 7)]
+    new = ko.apply_defrag(tables, src, dst)
+    assert sorted(x for t in new for x in t) == valid[:70]  # dense prefix of the id space
+    # brute force: byte payloads follow their blocks
+    pool = {b: rng.integers(0, 1 << 30) for b in valid}
+    moved = dict(pool)
+    for s, d in zip(src, dst):
+        moved[d] = pool[s]
+    for old, nw in zip(tables, new):
+        assert [pool[x] for x in old] == [moved[x] for x in nw]
+    # already-dense pools move nothing
+    assert ko.plan_defrag(valid[:30], valid) == ([], [])
