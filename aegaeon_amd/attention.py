@@ -150,6 +150,16 @@ def attention_workspace_bytes(batch: int, n_q_heads: int, head_dim: int, max_seq
     return int(n)
 
 
+def attention_workspace(batch: int, n_q_heads: int, head_dim: int, max_seq_len: int,
+                        blocks_per_split: int = 0, device=None) -> Optional[torch.Tensor]:
+    """A zero-filled device workspace large enough for one call of these
+    sizes (None when the call needs none).  Reusable across calls."""
+    n = attention_workspace_bytes(batch, n_q_heads, head_dim, max_seq_len, blocks_per_split)
+    if n == 0:
+        return None
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
 def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                            block_tables: torch.Tensor, seq_lens: torch.Tensor, scale: float,
                            max_seq_len: int, out: Optional[torch.Tensor] = None,

@@ -35,36 +35,42 @@ struct AppendArgs {
   uint32_t total_chunks;   // n_layers * 2 * n_tokens * row_chunks
 };
 
+// The source row of a chunk does not depend on its slot, so the K/V loads and
+// the slot loads of all kAppendItems chunks are issued together; only the
+// stores wait for the slots.  That keeps the dependent-latency chain at one
+// HBM round trip plus the store.
 __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(AppendArgs a) {
   const uint32_t nthreads = gridDim.x * kAppendThreads;
   const uint32_t gid = blockIdx.x * kAppendThreads + threadIdx.x;
   u32x4 r[kAppendItems];
-  uint8_t* dst[kAppendItems];
+  int64_t s[kAppendItems];
+  uint32_t chunk[kAppendItems], tok[kAppendItems], lk[kAppendItems];
 #pragma unroll
   for (int k = 0; k < kAppendItems; ++k) {
     const uint32_t c = gid + k * nthreads;
-    dst[k] = nullptr;
+    s[k] = -1;
     if (c < a.total_chunks) {
-      const uint32_t chunk = c % a.row_chunks;
+      chunk[k] = c % a.row_chunks;
       const uint32_t rest = c / a.row_chunks;
-      const uint32_t tok = rest % a.n_tokens;
-      const uint32_t lk = rest / a.n_tokens;  // layer * 2 + kv
-      const uint32_t layer = lk >> 1, kv = lk & 1;
-      const int64_t s = a.slots[tok];
-      if (s >= 0 && s < a.n_slots) {
-        const int64_t blk = s / a.block_size, off = s - blk * a.block_size;
-        const uint8_t* src = kv ? a.value + layer * a.val_layer_b + tok * a.val_tok_b
-                                : a.key + layer * a.key_layer_b + tok * a.key_tok_b;
-        uint8_t* cache = kv ? a.vc : a.kc;
-        r[k] = *reinterpret_cast<const u32x4*>(src + (uint64_t)chunk * 16);
-        dst[k] = cache + layer * a.layer_b + blk * a.blk_b +
-                 off * (int64_t)a.row_chunks * 16 + (int64_t)chunk * 16;
-      }
+      tok[k] = rest % a.n_tokens;
+      lk[k] = rest / a.n_tokens;  // layer * 2 + kv
+      const uint32_t layer = lk[k] >> 1, kv = lk[k] & 1;
+      const uint8_t* src = kv ? a.value + layer * a.val_layer_b + tok[k] * a.val_tok_b
+                              : a.key + layer * a.key_layer_b + tok[k] * a.key_tok_b;
+      s[k] = a.slots[tok[k]];
+      r[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + chunk[k]);
     }
   }
 #pragma unroll
-  for (int k = 0; k < kAppendItems; ++k)
-    if (dst[k]) *reinterpret_cast<u32x4*>(dst[k]) = r[k];
+  for (int k = 0; k < kAppendItems; ++k) {
+    if (s[k] >= 0 && s[k] < a.n_slots) {
+      const int64_t blk = s[k] / a.block_size, off = s[k] - blk * a.block_size;
+      const uint32_t layer = lk[k] >> 1, kv = lk[k] & 1;
+      uint8_t* dst = (kv ? a.vc : a.kc) + layer * a.layer_b + blk * a.blk_b +
+                     off * (int64_t)a.row_chunks * 16;
+      reinterpret_cast<u32x4*>(dst)[chunk[k]] = r[k];
+    }
+  }
 }
 
 // One workgroup per (logical block, sequence, layer*2+kv): the tokens of a

@@ -175,6 +175,25 @@ def qwen_append_batch(seed: int = 0, batch: int = 256) -> DecodeBatch:
     return _decode_batch(QWEN25_7B, ctx, rng, 2.0, seed)
 
 
+def successive_step_slots(wb: DecodeBatch, n_steps: int) -> np.ndarray:
+    """Slot mappings ``[n_steps, B]`` of ``n_steps`` successive decode steps of
+    ``wb``: step r appends position ``context_len + r``.  Blocks that the
+    longer sequences need are taken, in order, from the pool ids no table
+    holds (tables grow at the tail, block_manager.py:651-694)."""
+    bs = wb.geometry.block_size
+    used = {b for t in wb.block_tables for b in t}
+    spare = iter(b for b in range(wb.n_pool_blocks) if b not in used)
+    tables = [list(t) for t in wb.block_tables]
+    out = np.empty((n_steps, wb.batch), dtype=np.int64)
+    for r in range(n_steps):
+        for i, c in enumerate(wb.context_lens):
+            pos = int(c) + r
+            while len(tables[i]) <= pos // bs:
+                tables[i].append(next(spare))
+            out[r, i] = tables[i][pos // bs] * bs + pos % bs
+    return out
+
+
 def qwen_attention_batch(seed: int = 0, batch: int = 128) -> DecodeBatch:
     """Qwen2.5-7B paged decode attention: 128 sequences whose seq_len (cached
     tokens including the current one) is lognormal(mean 1500, sigma 1) clipped

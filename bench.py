@@ -1,20 +1,35 @@
 """Benchmark of the MI355X KV-cache data path (one GPU).
 
-Headline (``value``): KV append throughput in GB/s for one decode step of the
-Qwen2.5-7B-shaped batch (28 layers, 4 KV heads, D 128, bf16, 256 sequences,
-context lengths lognormal mean 600, pool = 2x need), all layers in one launch.
-A "step" is one such append.  Algorithmic bytes per step: read K and V, write
-them into the paged pool, read the slot mapping:
-``2 * B * L * 2 * Hkv * D * 2 + 8 * B``.
+Headline (``value``): KV append throughput in GB/s for the Qwen2.5-7B-shaped
+decode step (28 layers, 4 KV heads, D 128, bf16, block 16, 256 sequences with
+context lengths lognormal(mean 600, sigma 1) clipped to [16, 4096], pool = 2x
+the need, scattered block tables), all layers in one launch.  A "step" is one
+such append.  Algorithmic bytes per step: read K and V, write them into the
+paged pool, read the slot mapping: ``2 * B * L * 2 * Hkv * D * 2 + 8 * B``.
 
-Secondary lines in the same JSON object (``ops``): paged decode attention
-microseconds per layer for the Qwen2.5-7B attention batch (128 sequences,
-lognormal mean 1500, up to 8192 tokens), block pack/scatter for the
-Llama-2-13B swap workload, defrag of the unified multi-model pool.
+The timed steps rotate over 32 successive decode steps (distinct K/V inputs and
+slot mappings, ~0.9 GB of distinct traffic), so the 256 MB last-level cache
+cannot serve the inputs from a previous step: every step reads and writes HBM.
 
-Timing: W untimed warm-up steps, then K timed steps bracketed by
-``torch.cuda.synchronize()``; kernel time per launch is taken with HIP events
-recorded on the stream the kernels run on (torch's current stream).
+Timing.  The host enqueues a launch in ~10 us of Python; a 8 us kernel would
+then measure the host.  Each timed region therefore starts behind a bounded
+spin kernel (torch.cuda._sleep) that holds the stream while the host enqueues
+all K launches; the GPU then runs them back to back:
+  * ms_per_step: HIP events at both ends of the K launches, divided by K
+    (device time per step including the gaps between launches);
+  * roofline.achieved: algorithmic bytes over the mean of per-launch HIP event
+    pairs (device duration of one launch), on the stream the kernels run on.
+torch.cuda.synchronize() brackets every timed region.
+
+Secondary lines (``ops``): the per-layer launch pattern of vLLM; paged decode
+attention (Qwen2.5-7B GQA 28/4, 128 sequences, lognormal mean 1500, up to 8192
+tokens) in us per layer; block pack and scatter for the Llama-2-13B swap
+workload (32 x 2048 tokens, 4096 blocks of 12.5 MiB) plus a sampled PCIe leg to
+pinned host; defrag of the unified multi-model pool followed by a Yi-1.5-9B
+decode step (append + attention); token gather.
+
+The CPU baseline is the numpy oracle's append timed on the host on a bounded
+sample of the same workload.
 """
 from __future__ import annotations
 
@@ -25,114 +40,343 @@ import os
 import platform
 import sys
 import time
+from pathlib import Path
 
 import numpy as np
 
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
 HBM_PEAK_GBS = 8000.0
+METRIC = "KV gather/append GB/s (%HBM peak); paged decode-attn µs/layer @Qwen2.5-7B"
+ROTATE_STEPS = 32
 
 
-def _events_ms(fn, iters: int) -> float:
-    import torch
-    st = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for _ in range(iters):
-        fn()
-    e1.record(st)
-    e1.synchronize()
-    return e0.elapsed_time(e1) / iters
+def log(msg: str) -> None:
+    print(f"# {msg}", file=sys.stderr, flush=True)
 
 
-def bench_append(args, device):
+class Timer:
+    """Device timing of back-to-back launches on torch's current stream."""
+
+    def __init__(self):
+        import torch
+        self.torch = torch
+        self.cycles_per_ms = self._calibrate()
+
+    def _calibrate(self) -> float:
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        torch.cuda._sleep(2_000_000)
+        e1.record()
+        e1.synchronize()
+        return 2_000_000 / max(e0.elapsed_time(e1), 1e-3)
+
+    def _hold(self, fn, steps: int) -> None:
+        """Enqueue a spin long enough to cover the host enqueue of `steps` calls."""
+        torch = self.torch
+        t0 = time.perf_counter()
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        host_ms = (time.perf_counter() - t0) / 3 * 1e3
+        hold_ms = min(2000.0, 2.0 * host_ms * steps + 2.0)
+        torch.cuda._sleep(int(hold_ms * self.cycles_per_ms))
+
+    def run(self, fn, steps: int):
+        """Returns (ms per step over the whole region, mean per-launch ms, wall s)."""
+        torch = self.torch
+        Ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self._hold(fn, steps)
+        start, end = Ev(), Ev()
+        start.record()
+        for i in range(steps):
+            fn(i)
+        end.record()
+        torch.cuda.synchronize()
+        region_ms = start.elapsed_time(end) / steps
+        wall = time.perf_counter() - t0
+        # per-launch event pairs
+        pairs = [(Ev(), Ev()) for _ in range(steps)]
+        self._hold(fn, 2 * steps)
+        for i, (a, b) in enumerate(pairs):
+            a.record()
+            fn(i)
+            b.record()
+        torch.cuda.synchronize()
+        per = [a.elapsed_time(b) for a, b in pairs]
+        return region_ms, float(np.mean(per)), wall
+
+
+# ----------------------------------------------------------------------------- append
+def bench_append(args, timer):
     import torch
     from aegaeon_amd import attention as A
-    from aegaeon_amd.workloads import qwen_append_batch
+    from aegaeon_amd.workloads import qwen_append_batch, successive_step_slots
+    dev = torch.device("cuda", 0)
     wb = qwen_append_batch(args.seed)
     g = wb.geometry
-    cache = torch.empty((wb.n_pool_blocks, *g.block_shape), dtype=torch.bfloat16, device=device)
-    gen = torch.Generator(device=device).manual_seed(args.seed)
-    key = torch.randn((g.n_layers, wb.batch, g.n_kv_heads, g.head_dim), generator=gen,
-                      device=device).to(torch.bfloat16)
-    val = torch.randn(key.shape, generator=gen, device=device).to(torch.bfloat16)
-    slots = torch.from_numpy(wb.slot_mapping()).to(device)
+    cache = torch.empty((wb.n_pool_blocks, *g.block_shape), dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    R = ROTATE_STEPS
+    keys = torch.randn((R, g.n_layers, wb.batch, g.n_kv_heads, g.head_dim), generator=gen,
+                       device=dev).to(torch.bfloat16)
+    vals = torch.randn(keys.shape, generator=gen, device=dev).to(torch.bfloat16)
+    slots = torch.from_numpy(successive_step_slots(wb, R)).to(dev)
 
-    def step():
-        A.append_kv(key, val, cache, slots)
+    def cold(i):
+        r = i % R
+        A.append_kv(keys[r], vals[r], cache, slots[r])
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    kernel_ms = _events_ms(step, args.steps)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    nbytes = wb.append_bytes()
-    # per-layer launches (vLLM's call pattern) for comparison
+    def hot(i):
+        A.append_kv(keys[0], vals[0], cache, slots[0])
+
     view = cache.permute(1, 2, 0, 3, 4, 5)
 
-    def per_layer():
+    def per_layer(i):
+        r = i % R
         for layer in range(g.n_layers):
-            A.reshape_and_cache_flash(key[layer], val[layer], view[layer, 0], view[layer, 1], slots)
+            A.reshape_and_cache_flash(keys[r, layer], vals[r, layer], view[layer, 0],
+                                      view[layer, 1], slots[r])
 
-    per_layer()
+    for i in range(args.warmup):
+        cold(i)
     torch.cuda.synchronize()
-    per_layer_ms = _events_ms(per_layer, max(1, args.steps // 4))
-    del cache
-    return {
-        "wb": wb, "bytes": nbytes, "kernel_ms": kernel_ms, "wall_s": wall,
-        "per_layer_launch_ms": per_layer_ms,
-    }
+    region_ms, launch_ms, wall = timer.run(cold, args.steps)
+    hot_region, hot_launch, _ = timer.run(hot, args.steps)
+    pl_region, pl_launch, _ = timer.run(per_layer, max(4, args.steps // 8))
+    nbytes = wb.append_bytes()
+    del cache, keys, vals
+    torch.cuda.empty_cache()
+    return {"wb": wb, "bytes": nbytes, "region_ms": region_ms, "launch_ms": launch_ms,
+            "wall_s": wall, "hot_launch_ms": hot_launch, "hot_region_ms": hot_region,
+            "per_layer_step_ms": pl_region}
 
 
-def bench_attention(args, device):
+# -------------------------------------------------------------------------- attention
+def _fill_random(t, gen, chunk_blocks=1024):
+    import torch
+    for i in range(0, t.size(0), chunk_blocks):
+        sl = t[i:i + chunk_blocks]
+        sl.copy_(torch.randn(sl.shape, generator=gen, device=t.device, dtype=torch.float32)
+                 .to(t.dtype))
+
+
+def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
     import torch
     from aegaeon_amd import attention as A
     from aegaeon_amd.workloads import qwen_attention_batch
-    wb = qwen_attention_batch(args.seed)
+    dev = torch.device("cuda", 0)
+    wb = wb or qwen_attention_batch(args.seed)
     g = wb.geometry
     N = wb.n_pool_blocks
-    cache = torch.empty((N, *g.block_shape), dtype=torch.bfloat16, device=device)
-    gen = torch.Generator(device=device).manual_seed(args.seed + 1)
-    # random K/V in the used blocks (all layers), in slices to bound the temporary
-    for i in range(0, N, 1024):
-        sl = cache[i:i + 1024]
-        sl.copy_(torch.randn(sl.shape, generator=gen, device=device, dtype=torch.float32)
-                 .to(torch.bfloat16))
+    cache = torch.empty((N, *g.block_shape), dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    _fill_random(cache, gen)
     q = torch.randn((g.n_layers, wb.batch, g.n_q_heads, g.head_dim), generator=gen,
-                    device=device).to(torch.bfloat16)
-    bt = torch.from_numpy(wb.padded_tables()).to(device)
-    sl = torch.from_numpy(wb.seq_lens.astype(np.int32)).to(device)
+                    device=dev).to(torch.bfloat16)
+    bt = torch.from_numpy(wb.padded_tables()).to(dev)
+    sl = torch.from_numpy(wb.seq_lens.astype(np.int32)).to(dev)
     max_len = int(wb.seq_lens.max())
     view = cache.permute(1, 2, 0, 3, 4, 5)
     scale = 1.0 / math.sqrt(g.head_dim)
     outs = torch.empty_like(q)
-    ws = torch.empty(max(1, A.attention_workspace_bytes(wb.batch, g.n_q_heads, g.head_dim,
-                                                        max_len, args.bps)),
-                     dtype=torch.uint8, device=device)
+    ws = A.attention_workspace(wb.batch, g.n_q_heads, g.head_dim, max_len, args.bps, device=dev)
 
-    def all_layers():
-        for layer in range(g.n_layers):
-            A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], bt, sl, scale,
-                                     max_len, out=outs[layer], blocks_per_split=args.bps,
-                                     workspace=ws)
+    def layer_call(i):
+        layer = i % g.n_layers
+        A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], bt, sl, scale,
+                                 max_len, out=outs[layer], blocks_per_split=args.bps,
+                                 workspace=ws)
 
-    all_layers()
+    for i in range(g.n_layers):
+        layer_call(i)
     torch.cuda.synchronize()
-    ms = _events_ms(all_layers, max(1, args.steps // 4))
-    per_layer_us = ms * 1e3 / g.n_layers
+    steps = max(g.n_layers, (args.steps // g.n_layers) * g.n_layers)
+    region_ms, launch_ms, _ = timer.run(layer_call, steps)
     nbytes = wb.attention_bytes()
     del cache
-    return {"wb": wb, "bytes_per_layer": nbytes, "us_per_layer": per_layer_us}
+    torch.cuda.empty_cache()
+    return {"label": label, "wb": wb, "bytes_per_layer": nbytes, "us_per_layer": region_ms * 1e3,
+            "launch_us": launch_ms * 1e3}
 
 
+# ------------------------------------------------------------------------ pack / swap
+def bench_pack(args, timer):
+    """Llama-2-13B: pack the 4096 scattered blocks into a contiguous device
+    staging buffer, scatter them into a disjoint free set; sampled PCIe leg."""
+    import torch
+    from aegaeon_amd import ops
+    from aegaeon_amd.workloads import llama_swap_workload
+    dev = torch.device("cuda", 0)
+    wl = llama_swap_workload(args.seed, n_seqs=args.swap_seqs)
+    g = wl.geometry
+    bb = g.block_bytes
+    pool = torch.empty((wl.n_pool_blocks, bb), dtype=torch.uint8, device=dev)
+    pool.view(torch.int32).fill_(0x3C003C00)
+    staging = torch.empty((wl.n_blocks, bb), dtype=torch.uint8, device=dev)
+    src = np.asarray(wl.gpu_ids, dtype=np.int64)
+    dst = np.asarray(wl.swap_in_ids, dtype=np.int64)
+
+    def pack(i):
+        ops.pack_blocks(pool, src, out=staging)
+
+    def scatter(i):
+        ops.scatter_blocks(staging, dst, pool)
+
+    pack(0)
+    scatter(0)
+    torch.cuda.synchronize()
+    steps = max(2, args.steps // 40)
+    p_region, p_launch, _ = timer.run(pack, steps)
+    s_region, s_launch, _ = timer.run(scatter, steps)
+    nbytes = wl.pack_bytes()
+    # PCIe leg on a sample: D2H of packed blocks into pinned host, then H2D back
+    n_s = min(args.pcie_blocks, wl.n_blocks)
+    host = torch.empty((n_s, bb), dtype=torch.uint8, pin_memory=True)
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    e[0].record()
+    host.copy_(staging[:n_s], non_blocking=True)
+    e[1].record()
+    staging[:n_s].copy_(host, non_blocking=True)
+    e[2].record()
+    torch.cuda.synchronize()
+    d2h = n_s * bb / (e[0].elapsed_time(e[1]) * 1e-3) / 1e9
+    h2d = n_s * bb / (e[1].elapsed_time(e[2]) * 1e-3) / 1e9
+    del pool, staging, host
+    torch.cuda.empty_cache()
+    return {"wl": wl, "bytes": nbytes, "pack_ms": p_launch, "scatter_ms": s_launch,
+            "pack_region_ms": p_region, "pcie_blocks": n_s, "d2h_gbs": d2h, "h2d_gbs": h2d}
+
+
+# ------------------------------------------------------------- unified pool + defrag
+def bench_defrag(args, timer):
+    """Unified pool co-hosting Yi-1.5-9B, Qwen2.5-7B and Llama-2-13B blocks in
+    1 GiB slabs at 50% occupancy: compact each model's live blocks into the
+    dense prefix of its id space, then one Yi decode step (append + attention)
+    through the rewritten tables."""
+    import torch
+    from aegaeon_amd import attention as A
+    from aegaeon_amd import ops
+    from aegaeon_amd.pool import plan_compaction, remap_tables
+    from aegaeon_amd.workloads import DecodeBatch, unified_pool_workload
+    dev = torch.device("cuda", 0)
+    wl = unified_pool_workload(args.seed)
+    pool = torch.empty(wl.pool_bytes, dtype=torch.uint8, device=dev)
+    pool.view(torch.int32).fill_(0x3F803F80)
+    moved_bytes, ms, plans = 0, 0.0, {}
+    for name, g in wl.geometries.items():
+        live = [b for t in wl.tables[name] for b in t]
+        src, dst = plan_compaction(live, wl.valid_ids(name))
+        plans[name] = (src, dst)
+    # time the three shape-wise compactions as one step (they touch disjoint slabs)
+    snapshot = {n: (np.asarray(s), np.asarray(d)) for n, (s, d) in plans.items()}
+
+    def defrag(i):
+        for name, (s, d) in snapshot.items():
+            if len(s):
+                # forward on even steps, back on odd ones, so every step moves bytes
+                a, b = (s, d) if i % 2 == 0 else (d, s)
+                ops.defrag_blocks(pool, a, b, block_bytes=wl.geometries[name].block_bytes)
+
+    defrag(0)
+    defrag(1)
+    torch.cuda.synchronize()
+    steps = max(2, args.steps // 20)
+    region_ms, launch_ms, _ = timer.run(defrag, steps)
+    for name, (s, d) in snapshot.items():
+        moved_bytes += 2 * len(s) * wl.geometries[name].block_bytes + 16 * len(s)
+    n_moved = {n: int(len(s)) for n, (s, _) in snapshot.items()}
+
+    # Yi decode step through the compacted tables, on the same byte pool
+    g = wl.geometries[wl.decode_model]
+    src, dst = plans[wl.decode_model]
+    tables = remap_tables(wl.tables[wl.decode_model], src, dst)
+    nb = wl.pool_bytes // g.block_bytes
+    typed = pool[:nb * g.block_bytes].view(torch.bfloat16).view(nb, *g.block_shape)
+    ctx = wl.yi_context_lens
+    wb = DecodeBatch(g, ctx, tables, nb, args.seed)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 2)
+    key = torch.randn((g.n_layers, wb.batch, g.n_kv_heads, g.head_dim), generator=gen,
+                      device=dev).to(torch.bfloat16)
+    val = torch.randn(key.shape, generator=gen, device=dev).to(torch.bfloat16)
+    slots = torch.from_numpy(wb.slot_mapping()).to(dev)
+    q = torch.randn((g.n_layers, wb.batch, g.n_q_heads, g.head_dim), generator=gen,
+                    device=dev).to(torch.bfloat16)
+    bt = torch.from_numpy(wb.padded_tables()).to(dev)
+    sl = torch.from_numpy(wb.seq_lens.astype(np.int32)).to(dev)
+    max_len = int(wb.seq_lens.max())
+    view = typed.permute(1, 2, 0, 3, 4, 5)
+    out = torch.empty_like(q)
+    ws = A.attention_workspace(wb.batch, g.n_q_heads, g.head_dim, max_len, args.bps, device=dev)
+    scale = 1.0 / math.sqrt(g.head_dim)
+
+    def app(i):
+        A.append_kv(key, val, typed, slots)
+
+    def attn(i):
+        layer = i % g.n_layers
+        A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], bt, sl, scale,
+                                 max_len, out=out[layer], blocks_per_split=args.bps,
+                                 workspace=ws)
+
+    app(0)
+    attn(0)
+    torch.cuda.synchronize()
+    a_region, a_launch, _ = timer.run(app, max(4, args.steps // 4))
+    t_region, t_launch, _ = timer.run(attn, g.n_layers * max(1, args.steps // 100))
+    del pool, typed
+    torch.cuda.empty_cache()
+    return {"defrag_ms": launch_ms, "defrag_bytes": moved_bytes, "moved_blocks": n_moved,
+            "yi_append_ms": a_launch, "yi_append_bytes": wb.append_bytes(),
+            "yi_attn_us_per_layer": t_region * 1e3, "yi_attn_bytes": wb.attention_bytes(),
+            "yi_batch": wb.batch}
+
+
+# --------------------------------------------------------------------------- gather
+def bench_gather(args, timer):
+    """De-page every sequence of the Qwen2.5-7B append batch (one layer, K and
+    V) into contiguous [sum(len), Hkv, D] buffers."""
+    import torch
+    from aegaeon_amd import attention as A
+    from aegaeon_amd.workloads import qwen_append_batch
+    dev = torch.device("cuda", 0)
+    wb = qwen_append_batch(args.seed)
+    g = wb.geometry
+    cache = torch.empty((wb.n_pool_blocks, *g.block_shape), dtype=torch.bfloat16, device=dev)
+    cache.view(torch.int16).fill_(0x3F80)
+    bt = torch.from_numpy(wb.padded_tables()).to(dev)
+    sl_np = wb.seq_lens
+    sl = torch.from_numpy(sl_np.astype(np.int32)).to(dev)
+    total, max_len = int(sl_np.sum()), int(sl_np.max())
+    outs = {}
+
+    def gather(i):
+        layer = i % g.n_layers
+        outs[0] = A.gather_tokens(cache, bt, sl, total, max_len, layers=(layer, 1))
+
+    gather(0)
+    torch.cuda.synchronize()
+    region_ms, launch_ms, _ = timer.run(gather, max(g.n_layers, args.steps // 4))
+    nbytes = 2 * 2 * total * g.row_elems * 2 + 4 * sum(-(-int(x) // 16) for x in sl_np)
+    del cache
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "launch_ms": launch_ms, "region_ms": region_ms}
+
+
+# ---------------------------------------------------------------------- CPU baseline
 def cpu_baseline_append(args):
     """The oracle's append (numpy, one thread) on a bounded sample: the same
     256 tokens x 28 layers, into a compact pool holding only the touched
-    blocks; repeated for ~10 s."""
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import kv_oracle as ko
+    blocks; repeated for about --cpu-seconds."""
     from aegaeon_amd.workloads import qwen_append_batch
+    from oracle import kv_oracle as ko
     wb = qwen_append_batch(args.seed)
     g = wb.geometry
     slots = wb.slot_mapping()
@@ -151,10 +395,34 @@ def cpu_baseline_append(args):
         el = time.perf_counter() - t0
         if el > args.cpu_seconds:
             break
-    return {"value": wb.append_bytes() * reps / el / 1e9, "unit": "GB/s", "cores": 1,
+    return {"value": round(wb.append_bytes() * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": f"oracle append_layers (numpy, 1 thread), {reps} reps of the full 256-token "
-                      f"x 28-layer append into a compact {len(blocks)}-block pool, {el:.1f} s"}
+            "sample": f"numpy oracle append_layers on 1 host thread: {reps} repetitions of the "
+                      f"full 256-token x 28-layer Qwen2.5-7B append into a compact "
+                      f"{len(blocks)}-block pool in {el:.1f} s",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _traffic():
+    """HBM bytes per append launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None."""
+    p = ROOT / "profiles" / "kv_append_qwen_pmc.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def main(argv=None):
@@ -166,67 +434,110 @@ def main(argv=None):
     p.add_argument("--bps", type=int, default=0, help="attention blocks per split (0 = default)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["append", "attention", "all"], default="all")
+    p.add_argument("--swap-seqs", type=int, default=32)
+    p.add_argument("--pcie-blocks", type=int, default=64)
+    p.add_argument("--only", default="all",
+                   help="comma list of append,attention,pack,defrag,gather or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU "
-                                   "and runs no collectives; --gpus must be 1"}))
+        print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU and "
+                                   "runs no collectives, so --gpus must be 1"}), flush=True)
         return 2
     import torch
     if not torch.cuda.is_available():
-        print(json.dumps({"error": "no GPU visible"}))
+        print(json.dumps({"error": "no GPU visible"}), flush=True)
         return 2
     from aegaeon_amd import _lib
     _lib.load()
-    device = torch.device("cuda", 0)
-    torch.cuda.set_device(device)
-    print(f"# device: {torch.cuda.get_device_name(device)}", file=sys.stderr, flush=True)
-
+    torch.cuda.set_device(0)
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    only = set(args.only.split(",")) if args.only != "all" else \
+        {"append", "attention", "pack", "defrag", "gather"}
+    timer = Timer()
+    log(f"spin calibration: {timer.cycles_per_ms:.0f} cycles/ms")
     res = {}
-    if args.only in ("append", "all"):
-        res["append"] = bench_append(args, device)
-        print(f"# append done: {res['append']['kernel_ms']*1e3:.2f} us/launch", file=sys.stderr,
-              flush=True)
-    if args.only in ("attention", "all"):
-        res["attention"] = bench_attention(args, device)
-        print(f"# attention done: {res['attention']['us_per_layer']:.2f} us/layer",
-              file=sys.stderr, flush=True)
+    for name, fn in (("append", bench_append), ("attention", bench_attention),
+                     ("gather", bench_gather), ("pack", bench_pack), ("defrag", bench_defrag)):
+        if name in only:
+            t0 = time.perf_counter()
+            res[name] = fn(args, timer)
+            log(f"{name} done in {time.perf_counter() - t0:.1f} s")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_append(args)
-        print(f"# cpu baseline done: {cpu['value']:.3f} GB/s", file=sys.stderr, flush=True)
+        log(f"cpu baseline done: {cpu['value']} GB/s")
 
-    line = {"metric": "KV gather/append GB/s (%HBM peak); paged decode-attn us/layer @Qwen2.5-7B",
-            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-            "data": "synthetic (seeded N(0,1) K/V, seeded lognormal lengths and block tables)"}
+    line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic: seeded N(0,1) K/V and queries, seeded lognormal lengths and "
+                    "random-permutation block tables"}
+    ops_out = {}
     if "append" in res:
         a = res["append"]
-        gbs = a["bytes"] / (a["kernel_ms"] * 1e-3) / 1e9
+        value = a["bytes"] / (a["region_ms"] * 1e-3) / 1e9
+        achieved = a["bytes"] / (a["launch_ms"] * 1e-3) / 1e9
         line.update({
-            "value": round(gbs, 2), "ms_per_step": round(a["kernel_ms"], 6),
-            "config": {"workload": "Qwen2.5-7B decode-step KV append, all 28 layers in one launch",
-                       "batch": a["wb"].batch, "layers": 28, "kv_heads": 4, "head_dim": 128,
-                       "block_size": 16, "pool_blocks": a["wb"].n_pool_blocks,
-                       "bytes_per_step": a["bytes"]},
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+            "value": round(value, 1), "ms_per_step": round(a["region_ms"], 6),
+            "config": {"workload": "Qwen2.5-7B-shaped decode-step KV append, all 28 layers in "
+                                   "one launch, 256 sequences (lognormal mean 600), bf16",
+                       "layers": 28, "kv_heads": 4, "head_dim": 128, "block_size": 16,
+                       "batch": a["wb"].batch, "pool_blocks": a["wb"].n_pool_blocks,
+                       "bytes_per_step": a["bytes"], "rotated_steps": ROTATE_STEPS},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": _traffic()},
         })
-        line["ops"] = {"append_per_layer_launches_us": round(a["per_layer_launch_ms"] * 1e3, 2)}
+        ops_out["append_kernel_us"] = round(a["launch_ms"] * 1e3, 2)
+        ops_out["append_same_inputs_every_step_us"] = round(a["hot_launch_ms"] * 1e3, 2)
+        ops_out["append_per_layer_28_launches_us"] = round(a["per_layer_step_ms"] * 1e3, 2)
     if "attention" in res:
         t = res["attention"]
         gbs = t["bytes_per_layer"] / (t["us_per_layer"] * 1e-6) / 1e9
-        line.setdefault("ops", {})["paged_decode_attention"] = {
-            "workload": "Qwen2.5-7B GQA 28/4, D 128, bf16, 128 seqs, lognormal mean 1500",
-            "us_per_layer": round(t["us_per_layer"], 2), "bytes_per_layer": t["bytes_per_layer"],
-            "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        ops_out["paged_decode_attention"] = {
+            "workload": "Qwen2.5-7B GQA 28/4, D 128, bf16, 128 seqs, lognormal mean 1500 "
+                        "(sum len 189059), 28 layers back to back",
+            "us_per_layer": round(t["us_per_layer"], 2),
+            "us_per_call_events": round(t["launch_us"], 2),
+            "bytes_per_layer": t["bytes_per_layer"], "GB/s": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         if "value" not in line:
             line.update({"value": round(t["us_per_layer"], 2), "unit": "us/layer",
                          "higher_is_better": False})
+    if "gather" in res:
+        gt = res["gather"]
+        gbs = gt["bytes"] / (gt["launch_ms"] * 1e-3) / 1e9
+        ops_out["gather_tokens_one_layer"] = {
+            "workload": "Qwen2.5-7B append batch, 256 seqs, one layer K+V",
+            "us": round(gt["launch_ms"] * 1e3, 2), "bytes": gt["bytes"], "GB/s": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    if "pack" in res:
+        pk = res["pack"]
+        pg = pk["bytes"] / (pk["pack_ms"] * 1e-3) / 1e9
+        sg = pk["bytes"] / (pk["scatter_ms"] * 1e-3) / 1e9
+        ops_out["swap_pack_scatter"] = {
+            "workload": f"Llama-2-13B, {pk['wl'].n_blocks} blocks x 12.5 MiB fp16",
+            "pack_ms": round(pk["pack_ms"], 3), "scatter_ms": round(pk["scatter_ms"], 3),
+            "bytes": pk["bytes"], "pack_GB/s": round(pg, 1), "scatter_GB/s": round(sg, 1),
+            "pack_frac_hbm": round(pg / HBM_PEAK_GBS, 4),
+            "scatter_frac_hbm": round(sg / HBM_PEAK_GBS, 4),
+            "pcie_sample_blocks": pk["pcie_blocks"], "d2h_GB/s": round(pk["d2h_gbs"], 1),
+            "h2d_GB/s": round(pk["h2d_gbs"], 1)}
+    if "defrag" in res:
+        d = res["defrag"]
+        dg = d["defrag_bytes"] / (d["defrag_ms"] * 1e-3) / 1e9
+        ag = d["yi_append_bytes"] / (d["yi_append_ms"] * 1e-3) / 1e9
+        tg = d["yi_attn_bytes"] / (d["yi_attn_us_per_layer"] * 1e-6) / 1e9
+        ops_out["unified_pool_defrag"] = {
+            "workload": "Yi-1.5-9B + Qwen2.5-7B + Llama-2-13B blocks in 1 GiB slabs, 50% live",
+            "moved_blocks": d["moved_blocks"], "ms": round(d["defrag_ms"], 3),
+            "bytes": d["defrag_bytes"], "GB/s": round(dg, 1), "frac_hbm": round(dg / HBM_PEAK_GBS, 4),
+            "yi_append_us": round(d["yi_append_ms"] * 1e3, 2), "yi_append_GB/s": round(ag, 1),
+            "yi_attention_us_per_layer": round(d["yi_attn_us_per_layer"], 2),
+            "yi_attention_GB/s": round(tg, 1), "yi_attention_frac_hbm": round(tg / HBM_PEAK_GBS, 4)}
+    line["ops"] = ops_out
     if cpu is not None:
-        cpu["value"] = round(cpu["value"], 4)
         line["cpu_baseline"] = cpu
-        line["cpu_baseline"]["cpu_model"] = platform.processor() or platform.machine()
     print(json.dumps(line), flush=True)
     return 0
 

@@ -167,12 +167,14 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
  *   max_seq_len: host upper bound of seq_lens (sizes the split-KV grid); device
  *     lengths above it are clamped to it, so a wrong bound never reads or writes
  *     out of bounds.
- *   blocks_per_split: KV blocks per work item (0 = library default).
+ *   blocks_per_split: KV blocks per work item, 1..64 (0 = library default, 16).
  *   workspace: DEVICE scratch for split-KV partials of
  *     aegkv_paged_decode_attention_workspace_size(...) bytes.
- * Supported: block_size 16, head_dim 64/128/256, n_q_heads/n_kv_heads <= 16.
+ * Supported: block_size 16, head_dim 64/128/256, n_q_heads/n_kv_heads <= 16,
+ * blocks_per_split <= 64 (AEGKV_ERR_UNSUPPORTED otherwise).
  * seq_lens[b] == 0 yields zeros.  A block id outside [0, n_blocks) is never
- * dereferenced: its tokens are masked out of the softmax. */
+ * dereferenced: its tokens are masked out of the softmax.  n_blocks must be >= 1
+ * (AEGKV_ERR_INVALID_ARG otherwise). */
 int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_heads,
                                                      int32_t head_dim,
                                                      int32_t max_seq_len,

@@ -71,7 +71,7 @@ def _run(device, lens, Hq, Hkv, D, dtype, bps=0, seed=0, kc_override=None):
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 @pytest.mark.parametrize("Hq,Hkv,D", [(28, 4, 128), (32, 4, 128), (8, 8, 128), (16, 1, 64),
                                       (6, 2, 256)])
-@pytest.mark.parametrize("bps", [0, 1, 3])
+@pytest.mark.parametrize("bps", [0, 1, 3, 64])
 def test_matches_fp64_textbook(device, dtype, Hq, Hkv, D, bps):
     lens = [1, 15, 16, 17, 31, 64, 200, 517]
     out, ref, _ = _run(device, lens, Hq, Hkv, D, dtype, bps=bps, seed=Hq * 1000 + D + bps)

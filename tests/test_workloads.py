@@ -70,3 +70,27 @@ def test_unified_pool_slabs_hold_one_shape_each():
             s = b * g.block_bytes // wl.slab_bytes
             assert wl.slab_owner[s] == name
             assert (b + 1) * g.block_bytes <= (s + 1) * wl.slab_bytes
+
+
+def test_plan_compaction_matches_oracle_and_invariants():
+    from aegaeon_amd.pool import plan_compaction, remap_tables, slab_of, slab_range
+    from oracle import kv_oracle as ko
+    import pytest
+    rng = np.random.default_rng(0)
+    for trial in range(20):
+        valid = np.sort(rng.permutation(1000)[:300])
+        live = rng.permutation(valid)[:rng.integers(0, 301)]
+        src, dst = plan_compaction(live, valid)
+        osrc, odst = ko.plan_defrag(live, valid.tolist())
+        assert src.tolist() == list(osrc) and dst.tolist() == list(odst)
+        t = remap_tables([live.tolist()], src, dst)[0]
+        assert sorted(t) == valid[:len(live)].tolist()
+    with pytest.raises(ValueError):
+        plan_compaction([5, 5], list(range(10)))
+    with pytest.raises(ValueError):
+        plan_compaction([11], list(range(10)))
+    # slab geometry of the reference's 1 GiB slabs (block_manager.py:242-245)
+    S, bb = 1 << 30, 917504
+    a, b = slab_range(1, S, bb)
+    assert a * bb >= S and b * bb <= 2 * S and (b + 1) * bb > 2 * S
+    assert all(slab_of(x, S, bb) == 1 for x in (a, b - 1))
