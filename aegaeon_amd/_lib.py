@@ -43,7 +43,7 @@ SIGNATURES: Dict[str, tuple] = {
                                     c_void_p, c_int64, c_int64, c_int32, c_int32, c_int32,
                                     c_int32, c_int32, c_void_p]),
     "aegkv_paged_decode_attention_workspace_size": (c_int64, [c_int32, c_int32, c_int32, c_int32,
-                                                              c_int32, c_int32]),
+                                                              c_int32, c_int32, c_int32]),
     "aegkv_paged_decode_attention": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                              c_void_p, c_int64, c_int64, c_void_p, c_int32,
                                              c_void_p, c_int32, c_int32, c_int32, c_int32,

@@ -141,32 +141,43 @@ def gather_tokens(kv_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: 
     return out_k, out_v
 
 
-def attention_workspace_bytes(batch: int, n_q_heads: int, head_dim: int, max_seq_len: int,
-                              blocks_per_split: int = 0, block_size: int = 16) -> int:
-    n = _lib.load().aegkv_paged_decode_attention_workspace_size(
-        batch, n_q_heads, head_dim, max_seq_len, block_size, blocks_per_split)
+def attention_workspace_bytes(batch: int, n_q_heads: int, n_kv_heads: int, head_dim: int,
+                              max_seq_len: int, dtype: torch.dtype = torch.bfloat16,
+                              n_workgroups: int = 0, device=None) -> int:
+    """Workspace bytes of one attention call of these sizes on ``device``
+    (the default workgroup count depends on the device)."""
+    if dtype not in _DTYPES:
+        raise ValueError("dtype must be bfloat16 or float16")
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    with torch.cuda.device(dev):
+        n = _lib.load().aegkv_paged_decode_attention_workspace_size(
+            batch, n_q_heads, n_kv_heads, head_dim, max_seq_len, _DTYPES[dtype], n_workgroups)
     if n < 0:
         _lib.check(int(n), "attention_workspace_bytes")
     return int(n)
 
 
-def attention_workspace(batch: int, n_q_heads: int, head_dim: int, max_seq_len: int,
-                        blocks_per_split: int = 0, device=None) -> Optional[torch.Tensor]:
-    """A zero-filled device workspace large enough for one call of these
-    sizes (None when the call needs none).  Reusable across calls."""
-    n = attention_workspace_bytes(batch, n_q_heads, head_dim, max_seq_len, blocks_per_split)
+def attention_workspace(batch: int, n_q_heads: int, n_kv_heads: int, head_dim: int,
+                        max_seq_len: int, dtype: torch.dtype = torch.bfloat16,
+                        n_workgroups: int = 0, device=None) -> Optional[torch.Tensor]:
+    """A device workspace large enough for every call of these sizes (None
+    when the call needs none).  Reusable across calls on one stream."""
+    n = attention_workspace_bytes(batch, n_q_heads, n_kv_heads, head_dim, max_seq_len, dtype,
+                                  n_workgroups, device)
     if n == 0:
         return None
-    return torch.zeros(n, dtype=torch.uint8, device=device)
+    return torch.empty(n, dtype=torch.uint8, device=device)
 
 
 def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                            block_tables: torch.Tensor, seq_lens: torch.Tensor, scale: float,
                            max_seq_len: int, out: Optional[torch.Tensor] = None,
-                           blocks_per_split: int = 0,
+                           n_workgroups: int = 0,
                            workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Paged GQA decode attention: ``q [B, Hq, D]`` against per-layer cache
-    views ``[N, 16, Hkv, D]``; returns ``out [B, Hq, D]`` in q's dtype."""
+    views ``[N, 16, Hkv, D]``; returns ``out [B, Hq, D]`` in q's dtype.
+    ``n_workgroups`` = 0 spreads the batch over the device's resident
+    workgroups; a positive count forces that many (same result)."""
     if q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.size(2) or not q.is_cuda:
         raise ValueError("q must be a GPU tensor [B, Hq, D] with dense heads")
     _check_cache_view(key_cache, "key_cache")
@@ -185,7 +196,10 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
         out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     elif out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D:
         raise ValueError("out must be [B, Hq, D] with dense heads")
-    ws_bytes = attention_workspace_bytes(B, Hq, D, max_seq_len, blocks_per_split, bs)
+    if B == 0:
+        return out
+    ws_bytes = attention_workspace_bytes(B, Hq, Hkv, D, max_seq_len, q.dtype, n_workgroups,
+                                         q.device)
     if ws_bytes > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if (workspace is not None and ws_bytes > 0) else None
@@ -194,7 +208,7 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
             out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), key_cache.data_ptr(),
             value_cache.data_ptr(), key_cache.stride(0), N, bt.data_ptr(), bt.size(1),
             sl.data_ptr(), B, max_seq_len, Hq, Hkv, D, bs, float(scale), _DTYPES[q.dtype],
-            blocks_per_split, ws_ptr, ws_bytes if ws_ptr else 0, _stream(q))
+            n_workgroups, ws_ptr, ws_bytes if ws_ptr else 0, _stream(q))
     _lib.check(rc, "paged_decode_attention")
     return out
 

@@ -2,11 +2,22 @@
 // flash_attn_with_kvcache on the decode path, selected at
 // aegaeon/aegaeon/worker.py:410-418 and run inside the forward at :517-523).
 //
-// Work item = one wave64 per (KV split, kv head, sequence); a 256-thread
-// workgroup holds the 4 kv heads of one (split, sequence), so its waves stream
-// the four adjacent 256-byte head slices of the same 1 KiB token rows.  All
-// G = Hq/Hkv query heads of a kv head are processed together, so each K/V byte
-// is read from HBM exactly once per decode step.
+// Work decomposition (persistent and balanced).  The batch's KV blocks are
+// laid end to end per group of kHeadsPerGroup kv heads, each sequence
+// preceded by kSegmentCost charge positions for the cost of starting it:
+// position P = grp * W + cum[b] + kSegmentCost + j for block j of sequence b,
+// W = sum_b (ceil(len_b / 16) + kSegmentCost).  One workgroup per CU takes an
+// equal contiguous range of positions, so every CU does the same work in a
+// single round, and consecutive ranges land on different XCDs (workgroups are
+// dealt to the XCDs round-robin).  Each workgroup computes the prefix sums of
+// the batch itself (into LDS) and walks its range; a range may cut sequences,
+// whose pieces write fp32 partials (unnormalised O, running max in log2
+// units, sum) that a second kernel merges with log-sum-exp weights.  A
+// sequence held by one workgroup is normalised and written directly.
+//
+// Inside a workgroup, wave w handles kv head grp * 4 + w, and all
+// G = Hq / Hkv query heads of that kv head are processed together, so each K/V
+// byte is read from HBM exactly once per decode step.
 //
 // Per 16-token block (block_size 16), with lane l = 16*g + j:
 //   S^T[16 tok x 16 heads] = K[16 x D] . Q^T[D x 16]  -> D/32 MFMA 16x16x32
@@ -22,11 +33,9 @@
 //     Lane (j, g) loads V rows 4g..4g+3, dims [D/16*j, +D/16); tile t of the
 //     output holds dims D/16*i + t for A-row i, so output lane (j, g) owns head
 //     j, dims D/16*(4g+r) + t.
-// The block ids of a wave's split are loaded once, one per lane, and read with
-// readlane; K/V of the next block are in flight while the current one is
-// computed.
-// Sequences longer than one split write fp32 partials (unnormalised O, running
-// max in log2 units, sum) that a second kernel merges with log-sum-exp weights.
+// The block ids of a segment are loaded 64 at a time, one per lane, and read
+// with readlane; a rolling register pipeline keeps pipeline_depth - 1 blocks of K/V
+// in flight while one is computed.
 #include <algorithm>
 #include <cmath>
 #include <utility>
@@ -43,15 +52,28 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBlockSize = 16;
-constexpr int kDefaultBlocksPerSplit = 16;
-constexpr int kMaxBlocksPerSplit = 64;  // one block id per lane
-constexpr int kHeadsPerGroup = 4;       // waves (kv heads) per workgroup
-#ifndef AEGKV_ATTN_PIPELINE
-#define AEGKV_ATTN_PIPELINE 4
-#endif
-constexpr int kPipeline = AEGKV_ATTN_PIPELINE;  // K/V register buffers per wave
+constexpr int kHeadsPerGroup = 4;   // waves (kv heads) per workgroup
+constexpr int kMaxBatch = 2048;     // sequences per launch (LDS prefix sums); larger
+                                    // batches are launched in chunks
+constexpr int kScanPerThread = kMaxBatch / (64 * kHeadsPerGroup);
+// Cost of starting a sequence piece (block ids and q loaded, pipeline
+// primed) in units of one block: the partition balances blocks plus this
+// charge per sequence, so a workgroup that holds several short sequences gets
+// correspondingly fewer blocks (measured ~2 blocks on the Qwen2.5-7B batch).
+constexpr int kSegmentCost = 2;
+
+// Cost units of a sequence of `len` tokens: its blocks plus the start charge.
+__device__ __forceinline__ int cost_units(int len) {
+  const int nblk = (len + kBlockSize - 1) / kBlockSize;
+  return nblk > 0 ? nblk + kSegmentCost : 0;
+}
+// K/V register buffers per wave: three blocks of K and V fit the register
+// budget of two waves per SIMD up to D = 128; D = 256 keeps two and runs one
+// wave per SIMD.
+template <int D>
+constexpr int pipeline_depth() { return D >= 256 ? 2 : 3; }
 constexpr float kRescaleSlack = 8.f;  // log2 headroom of the lazy softmax rescale
-constexpr int kCombineUnroll = 4;     // splits per group loaded together by the combine
+constexpr int kCombineUnroll = 4;     // pieces per group loaded together by the combine
 
 template <int DT>
 struct Elem;
@@ -104,28 +126,52 @@ struct AttnArgs {
   const int32_t* block_tables;
   int32_t max_blocks;
   const int32_t* seq_lens;
+  int32_t batch;
   int32_t n_q_heads;
   int32_t n_kv_heads;
-  int32_t group;  // n_q_heads / n_kv_heads
+  int32_t group;     // n_q_heads / n_kv_heads
+  int32_t hpg;       // query heads per workgroup: kHeadsPerGroup * group
+  int32_t n_groups;  // ceil(n_kv_heads / kHeadsPerGroup)
+  int32_t n_wg;      // workgroups of the main kernel
   float scale_log2;  // softmax scale * log2(e)
-  int32_t bps;       // blocks per split
-  int32_t max_splits;
   int32_t max_seq_len;  // host bound; longer device lengths are clamped to it
   uint16_t* out;
   int64_t out_bstride;  // elements
-  float* part_o;        // [batch][Hq][max_splits][D]
-  float2* part_ml;      // [batch][Hq][max_splits] (running max in log2 units, sum)
+  int32_t* cum;         // [batch + 1] block prefix sums, written by workgroup 0
+  float* part_o;        // [slots][hpg][D]
+  float2* part_ml;      // [slots][hpg] (running max in log2 units, sum)
 };
 
+// Workspace layout of one launch: the prefix sums, then the partials of
+// n_wg + n_groups * batch slots (a workgroup writes at most one slot per
+// sequence piece it holds; slot = workgroup + grp * batch + b is unique).
+struct WorkspaceLayout {
+  int64_t cum_bytes, ml_bytes, o_bytes, total;
+};
+inline WorkspaceLayout workspace_layout(int64_t batch, int64_t hpg, int64_t head_dim,
+                                        int64_t n_wg, int64_t n_groups) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  const int64_t slots = n_wg + n_groups * batch;
+  WorkspaceLayout w;
+  w.cum_bytes = up((batch + 1) * 4);
+  w.ml_bytes = up(slots * hpg * 8);
+  w.o_bytes = up(slots * hpg * head_dim * 4);
+  w.total = w.cum_bytes + w.ml_bytes + w.o_bytes;
+  return w;
+}
+
+// K/V are streamed once per decode step: non-temporal loads keep them from
+// displacing reusable lines in the caches (measured ~9% more read bandwidth
+// than ordinary loads on scattered 16-32 KiB regions).
 template <int NW>
 __device__ __forceinline__ void load_words(const uint16_t* p, uint32_t* w) {
   if constexpr (NW == 2) {
-    u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
     w[0] = v.x; w[1] = v.y;
   } else {
 #pragma unroll
     for (int i = 0; i < NW / 4; ++i) {
-      u32x4 v = *reinterpret_cast<const u32x4*>(p + 8 * i);
+      u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 8 * i));
       w[4 * i + 0] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
     }
   }
@@ -145,7 +191,7 @@ __device__ __forceinline__ void load_block(KVRegs<D>& r, const uint16_t* kh, con
                                            int64_t off, int64_t row) {
 #pragma unroll
   for (int ks = 0; ks < KVRegs<D>::KS; ++ks)
-    r.k[ks] = *reinterpret_cast<const u32x4*>(kh + off + 32 * ks);
+    r.k[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kh + off + 32 * ks));
 #pragma unroll
   for (int c = 0; c < 4; ++c) load_words<KVRegs<D>::VW>(vh + off + c * row, r.v[c]);
 }
@@ -231,35 +277,20 @@ __device__ __forceinline__ bool unrolled_steps(F&& f) {
   return unrolled_steps_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// One piece of a sequence for one kv head: blocks [j0, j1) of sequence b.
+// `complete` (the piece is the whole sequence) writes the normalised output,
+// otherwise the partial goes to `slot`.
 template <int DT, int D, int NBUF>
-__global__ __launch_bounds__(64 * kHeadsPerGroup) void paged_decode_attention_kernel(AttnArgs a) {
+__device__ __forceinline__ void attend_segment(const AttnArgs& a, int b, int h, int j0, int j1,
+                                               int len, bool complete, int64_t slot, int hl0) {
   using E = Elem<DT>;
   constexpr int KS = D / 32;
   constexpr int DPL = D / 16;
   constexpr int VW = D / 32;
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * kHeadsPerGroup + (threadIdx.x >> 6);
-  if (h >= a.n_kv_heads) return;  // whole waves; the kernel has no barrier
   const int j = lane & 15, g = lane >> 4;
-  // Sequence-major grid (split index fastest): the splits of a sequence are
-  // dispatched together.  Measured on the Qwen2.5-7B batch, a split-major
-  // order is 30-50% slower.
-  const int s = blockIdx.x, b = blockIdx.z;
-  const int len = min(max(a.seq_lens[b], 0), a.max_seq_len);
-  const int nblk = len > 0 ? (len + kBlockSize - 1) / kBlockSize : 0;
-  const int blk0 = s * a.bps;
-  if (s > 0 && blk0 >= nblk) return;
-  const int nb = max(0, min(nblk, blk0 + a.bps) - blk0);
-  const int nsplit = nblk > 0 ? (nblk + a.bps - 1) / a.bps : 1;
   const bool head_ok = j < a.group;
   const int hq = h * a.group + j;
-
-  // block ids of this split, one per lane; ids outside the pool become -1
-  int my_id = -1;
-  if (lane < nb) {
-    const int id = a.block_tables[(int64_t)b * a.max_blocks + blk0 + lane];
-    my_id = (id >= 0 && id < a.n_blocks) ? id : -1;
-  }
 
   u32x4 qv[KS];
   {
@@ -279,30 +310,55 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void paged_decode_attention_ke
   const int64_t row = (int64_t)a.n_kv_heads * D;
   const uint16_t* kh = a.kc + (int64_t)h * D + (int64_t)j * row + 8 * g;
   const uint16_t* vh = a.vc + (int64_t)h * D + (int64_t)(4 * g) * row + DPL * j;
+  const int32_t* bt = a.block_tables + (int64_t)b * a.max_blocks;
 
-  // Batches of NBUF blocks: the loads of a whole batch are issued first, then
-  // its blocks are computed in order, so the wait before block k covers only
-  // its own loads and NBUF-1-k blocks stay in flight behind it.  No load is
-  // pending across the loop's back edge (register buffers carried over it get
-  // copied at the latch, and copying a register that is still loading waits
-  // for it).  Every load is issued unconditionally: an unreadable id reads
-  // block 0 and is masked, a slot past the split re-reads its last block (an
-  // L2 hit) and is not computed.  The host guarantees n_blocks >= 1.
-  const int last = nb - 1;
-  for (int it = 0; it < nb; it += NBUF) {
+  for (int c0 = j0; c0 < j1; c0 += 64) {
+    const int nb = min(64, j1 - c0);
+    // block ids of this chunk, one per lane; ids outside the pool become -1
+    int my_id = -1;
+    if (lane < nb) {
+      const int id = bt[c0 + lane];
+      my_id = (id >= 0 && id < a.n_blocks) ? id : -1;
+    }
+    // Rolling register pipeline of NBUF blocks: buffer k holds block i = it + k;
+    // as soon as block i is computed, its buffer is refilled with block
+    // i + NBUF, so NBUF - 1 blocks stay in flight while a block is computed and
+    // the loads carried across the loop's back edge keep HBM busy between
+    // iterations.  The loop body is unrolled by NBUF, so every buffer keeps its
+    // registers across the back edge.  Inside the loop every load is issued
+    // unconditionally and no path leaves the body early (a refill past the
+    // chunk re-reads its last block, an L2 hit, and is never computed): the
+    // in-order vmcnt accounting then stays exact across the back edge and each
+    // wait covers only the buffer about to be computed.  The last nb % NBUF
+    // blocks are computed after the loop, which issues no further loads.  An
+    // unreadable id loads block 0 and is masked (the host guarantees
+    // n_blocks >= 1).
+    const int last = nb - 1;
+    const int nfull = nb - nb % NBUF;
     KVRegs<D> buf[NBUF];
     int ids[NBUF];
     unrolled_steps<NBUF>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
-      ids[k] = __builtin_amdgcn_readlane(my_id, min(it + k, last));
+      ids[k] = __builtin_amdgcn_readlane(my_id, min(k, last));
       load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
-      __builtin_amdgcn_sched_barrier(0);  // keep the blocks' loads in issue order
       return false;
     });
+    for (int it = 0; it < nfull; it += NBUF) {
+      unrolled_steps<NBUF>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int i = it + k;
+        compute_block<DT, D>(buf[k], qv, acc, m, lsum, (c0 + i) * kBlockSize,
+                             ids[k] >= 0 ? len : 0, g, a.scale_log2);
+        ids[k] = __builtin_amdgcn_readlane(my_id, min(i + NBUF, last));
+        load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
+        return false;
+      });
+    }
     unrolled_steps<NBUF>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
-      if (it + k >= nb) return true;
-      compute_block<DT, D>(buf[k], qv, acc, m, lsum, (blk0 + it + k) * kBlockSize,
+      const int i = nfull + k;
+      if (i >= nb) return true;
+      compute_block<DT, D>(buf[k], qv, acc, m, lsum, (c0 + i) * kBlockSize,
                            ids[k] >= 0 ? len : 0, g, a.scale_log2);
       return false;
     });
@@ -313,64 +369,169 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void paged_decode_attention_ke
 
   // lane holds head j, dims [4*DPL*g, 4*DPL*g + 4*DPL): dim offset DPL*r + t <- acc[t][r]
   const int d0 = 4 * DPL * g;
-  if (nsplit == 1) {
-    if (head_ok) {
-      const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      uint16_t* op = a.out + (int64_t)b * a.out_bstride + (int64_t)hq * D + d0;
+  if (!head_ok) return;
+  if (complete) {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t* op = a.out + (int64_t)b * a.out_bstride + (int64_t)hq * D + d0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint32_t w[VW];
+    for (int r = 0; r < 4; ++r) {
+      uint32_t w[VW];
 #pragma unroll
-        for (int t = 0; t < DPL; t += 2)
-          w[t >> 1] = E::bits(acc[t][r] * inv) | (E::bits(acc[t + 1][r] * inv) << 16);
-        if constexpr (VW == 2) {
-          *reinterpret_cast<u32x2*>(op + DPL * r) = u32x2{w[0], w[1]};
-        } else {
+      for (int t = 0; t < DPL; t += 2)
+        w[t >> 1] = E::bits(acc[t][r] * inv) | (E::bits(acc[t + 1][r] * inv) << 16);
+      if constexpr (VW == 2) {
+        *reinterpret_cast<u32x2*>(op + DPL * r) = u32x2{w[0], w[1]};
+      } else {
 #pragma unroll
-          for (int i = 0; i < VW / 4; ++i)
-            *reinterpret_cast<u32x4*>(op + DPL * r + 8 * i) =
-                u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
-        }
+        for (int i = 0; i < VW / 4; ++i)
+          *reinterpret_cast<u32x4*>(op + DPL * r + 8 * i) =
+              u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
       }
     }
   } else {
-    const int64_t pidx = ((int64_t)b * a.n_q_heads + hq) * a.max_splits + s;
-    if (head_ok) {
-      float* po = a.part_o + pidx * D + d0;
+    const int64_t pidx = slot * a.hpg + hl0 + j;
+    float* po = a.part_o + pidx * D + d0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int t = 0; t < DPL; t += 4)
-          *reinterpret_cast<f32x4*>(po + DPL * r + t) =
-              f32x4{acc[t][r], acc[t + 1][r], acc[t + 2][r], acc[t + 3][r]};
-      if (g == 0) a.part_ml[pidx] = make_float2(m, lt);
-    }
+      for (int t = 0; t < DPL; t += 4)
+        *reinterpret_cast<f32x4*>(po + DPL * r + t) =
+            f32x4{acc[t][r], acc[t + 1][r], acc[t + 2][r], acc[t + 3][r]};
+    if (g == 0) a.part_ml[pidx] = make_float2(m, lt);
   }
 }
 
-// Merge split partials of one (sequence, query head):
+template <int DT, int D, int NBUF>
+__global__ __launch_bounds__(64 * kHeadsPerGroup, D >= 256 ? 1 : 2) void
+paged_decode_attention_kernel(AttnArgs a) {
+  extern __shared__ int32_t s_mem[];  // cum[batch + 1], then len[batch]
+  __shared__ int32_t s_wave_tot[kHeadsPerGroup];
+  int32_t* s_cum = s_mem;
+  int32_t* s_len = s_mem + a.batch + 1;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+
+  // Cost prefix sums of the batch: thread t owns sequences
+  // [t * per, t * per + per); a wave scan plus the wave totals give each
+  // thread its exclusive offset.
+  {
+    const int per = (a.batch + 64 * kHeadsPerGroup - 1) / (64 * kHeadsPerGroup);
+    const int b0 = tid * per;
+    int lens[kScanPerThread];
+    int cnt = 0;
+#pragma unroll
+    for (int k = 0; k < kScanPerThread; ++k) {
+      lens[k] = 0;
+      if (k < per && b0 + k < a.batch) lens[k] = min(max(a.seq_lens[b0 + k], 0), a.max_seq_len);
+      cnt += cost_units(lens[k]);
+    }
+    int x = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave_tot[wave] = x;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += s_wave_tot[w];
+    int excl = base + x - cnt;
+#pragma unroll
+    for (int k = 0; k < kScanPerThread; ++k) {
+      if (k < per && b0 + k < a.batch) {
+        s_cum[b0 + k] = excl;
+        s_len[b0 + k] = lens[k];
+        excl += cost_units(lens[k]);
+      }
+    }
+    if (tid == 64 * kHeadsPerGroup - 1) s_cum[a.batch] = base + x;
+    __syncthreads();
+  }
+  if (blockIdx.x == 0)
+    for (int i = tid; i <= a.batch; i += 64 * kHeadsPerGroup) a.cum[i] = s_cum[i];
+
+  const int64_t W = s_cum[a.batch];
+  const int64_t total = W * a.n_groups;
+  // With fewer positions than workgroups only the first `total` take part, so
+  // that every range is non-empty.
+  const int64_t n_act = min((int64_t)a.n_wg, total);
+  if ((int64_t)blockIdx.x >= n_act) return;
+  int64_t P = (int64_t)blockIdx.x * total / n_act;
+  const int64_t p_end = (int64_t)(blockIdx.x + 1) * total / n_act;
+  // Every value below is uniform over the workgroup.  A sequence occupies
+  // positions [s_cum[b], s_cum[b + 1]): kSegmentCost charge positions, then
+  // one per block.
+  while (P < p_end) {
+    const int grp = (int)(P / W);
+    const int p = (int)(P - (int64_t)grp * W);
+    int lo = 0, hi = a.batch;  // s_cum[lo] <= p < s_cum[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_cum[mid] <= p) lo = mid; else hi = mid;
+    }
+    const int b = lo;
+    const int first = s_cum[b] + kSegmentCost;  // position of block 0
+    if (p < first) {  // charge positions hold no block
+      P += first - p;
+      continue;
+    }
+    const int nblk = s_cum[b + 1] - first;
+    const int j0 = p - first;
+    const int j1 = (int)min((int64_t)nblk, (int64_t)j0 + (p_end - P));
+    const int h = grp * kHeadsPerGroup + wave;
+    if (h < a.n_kv_heads)
+      attend_segment<DT, D, NBUF>(a, b, h, j0, j1, s_len[b], j0 == 0 && j1 == nblk,
+                                  (int64_t)blockIdx.x + (int64_t)grp * a.batch + b,
+                                  wave * a.group);
+    P += j1 - j0;
+  }
+}
+
+// Workgroup that holds position P of the flattened range (the largest w with
+// floor(w * total / n_act) <= P; n_act <= total, so every range is non-empty).
+__device__ __forceinline__ int64_t owner_of(int64_t P, int64_t total, int64_t n_act) {
+  return ((P + 1) * n_act - 1) / total;
+}
+
+// Finish one (sequence, query head): zeros for an empty sequence, nothing
+// when one workgroup held the whole sequence (it wrote the output), otherwise
+// merge the pieces' partials:
 //   out = sum_s w_s o_s / sum_s w_s l_s,  w_s = 2^(m_s - max m).
-// 256 threads = NG split groups x (D/4) lanes of 4 dims.  Each group loads up
-// to kCombineUnroll of its splits at once (independent loads, one memory
+// 256 threads = NG piece groups x (D/4) lanes of 4 dims.  Each group loads up
+// to kCombineUnroll of its pieces at once (independent loads, one memory
 // latency per pass), merges them online, and the groups merge in LDS.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   using E = Elem<DT>;
-  constexpr int LPS = D / 4;      // lanes per split row
-  constexpr int NG = 256 / LPS;   // split groups
+  constexpr int LPS = D / 4;      // lanes per piece row
+  constexpr int NG = 256 / LPS;   // piece groups
   constexpr int U = kCombineUnroll;
   __shared__ float s_m[NG], s_l[NG];
   __shared__ f32x4 s_o[NG][LPS];
   const int hq = blockIdx.x, b = blockIdx.y;
-  const int len = min(max(a.seq_lens[b], 0), a.max_seq_len);
-  const int nblk = len > 0 ? (len + kBlockSize - 1) / kBlockSize : 0;
-  const int nsplit = nblk > 0 ? (nblk + a.bps - 1) / a.bps : 1;
-  if (nsplit <= 1) return;  // uniform over the workgroup
-  const int grp = threadIdx.x / LPS, ln = threadIdx.x % LPS;
-  const int64_t base = ((int64_t)b * a.n_q_heads + hq) * a.max_splits;
+  const int grp_ln = threadIdx.x % LPS;
+  const int c0 = a.cum[b], c1 = a.cum[b + 1];
+  uint16_t* op = a.out + (int64_t)b * a.out_bstride + (int64_t)hq * D + 4 * grp_ln;
+  if (c1 == c0) {  // empty sequence (uniform over the workgroup)
+    if (threadIdx.x < LPS) *reinterpret_cast<u32x2*>(op) = u32x2{0u, 0u};
+    return;
+  }
+  // the pieces are the owners of the sequence's block positions
+  // [c0 + kSegmentCost, c1) of group grp
+  const int h = hq / a.group, grp = h / kHeadsPerGroup;
+  const int64_t total = (int64_t)a.cum[a.batch] * a.n_groups;
+  const int64_t n_act = min((int64_t)a.n_wg, total);
+  const int64_t P0 = (int64_t)grp * a.cum[a.batch] + c0 + kSegmentCost;
+  const int64_t w0 = owner_of(P0, total, n_act);
+  const int64_t w1 = owner_of((int64_t)grp * a.cum[a.batch] + c1 - 1, total, n_act);
+  if (w0 == w1) return;
+  const int npieces = (int)(w1 - w0 + 1);
+  const int64_t slot0 = w0 + (int64_t)grp * a.batch + b;
+  const int hl = hq - grp * kHeadsPerGroup * a.group;
+  const int pg = threadIdx.x / LPS, ln = grp_ln;
   float m = -INFINITY, l = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = grp; s0 < nsplit; s0 += NG * U) {
+  for (int s0 = pg; s0 < npieces; s0 += NG * U) {
     float2 ml[U];
     f32x4 po[U];
 #pragma unroll
@@ -378,14 +539,15 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
       const int s = s0 + u * NG;
       ml[u] = make_float2(-INFINITY, 0.f);
       po[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (s < nsplit) {
-        ml[u] = a.part_ml[base + s];
-        po[u] = *reinterpret_cast<const f32x4*>(a.part_o + (base + s) * D + 4 * ln);
+      if (s < npieces) {
+        const int64_t pidx = (slot0 + s) * a.hpg + hl;
+        ml[u] = a.part_ml[pidx];
+        po[u] = *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + 4 * ln);
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (ml[u].x == -INFINITY) continue;  // absent, or a split with no readable block
+      if (ml[u].x == -INFINITY) continue;  // absent, or a piece with no readable block
       const float mn = fmaxf(m, ml[u].x);
       const float wa = __builtin_amdgcn_exp2f(m - mn), wb = __builtin_amdgcn_exp2f(ml[u].x - mn);
       o = o * wa + po[u] * wb;
@@ -393,10 +555,10 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
       m = mn;
     }
   }
-  if (ln == 0) { s_m[grp] = m; s_l[grp] = l; }
-  s_o[grp][ln] = o;
+  if (ln == 0) { s_m[pg] = m; s_l[pg] = l; }
+  s_o[pg][ln] = o;
   __syncthreads();
-  if (grp == 0) {
+  if (pg == 0) {
     float mx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < NG; ++k) mx = fmaxf(mx, s_m[k]);
@@ -409,30 +571,38 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
       lt += s_l[k] * w;
     }
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    uint16_t* op = a.out + (int64_t)b * a.out_bstride + (int64_t)hq * D + 4 * ln;
     *reinterpret_cast<u32x2*>(op) =
         u32x2{E::bits(acc[0] * inv) | (E::bits(acc[1] * inv) << 16),
               E::bits(acc[2] * inv) | (E::bits(acc[3] * inv) << 16)};
   }
 }
 
-template <int DT, int D>
-int launch_attention(const AttnArgs& a, int batch, hipStream_t stream) {
-  const int groups = (a.n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
-  hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, kPipeline>),
-                     dim3(a.max_splits, groups, batch), dim3(64 * kHeadsPerGroup), 0, stream, a);
-  AEGKV_HIP_TRY(hipGetLastError());
-  if (a.max_splits > 1) {
-    hipLaunchKernelGGL((attention_combine_kernel<DT, D>), dim3(a.n_q_heads, batch), dim3(256),
-                       0, stream, a);
-    AEGKV_HIP_TRY(hipGetLastError());
+size_t lds_bytes(int32_t batch) { return (size_t)(2 * batch + 1) * sizeof(int32_t); }
+
+// Workgroups of the main kernel for one launch: one per CU (measured on the
+// Qwen2.5-7B batch: one workgroup of four waves per CU with three blocks in
+// flight per wave beats two or three per CU), or the caller's count.
+int workgroups_for(int32_t requested, int* n_wg) {
+  if (requested > 0) {
+    *n_wg = requested;
+    return AEGKV_OK;
   }
+  DeviceState* ds = nullptr;
+  int rc = current_device_state(&ds);
+  if (rc) return rc;
+  *n_wg = std::max(1, ds->num_cu);
   return AEGKV_OK;
 }
 
-int max_splits_for(int32_t max_seq_len, int32_t bps) {
-  const int nblk = (max_seq_len + kBlockSize - 1) / kBlockSize;
-  return std::max(1, (nblk + bps - 1) / bps);
+template <int DT, int D>
+int launch_attention(const AttnArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>()>), dim3(a.n_wg),
+                     dim3(64 * kHeadsPerGroup), lds_bytes(a.batch), stream, a);
+  AEGKV_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL((attention_combine_kernel<DT, D>), dim3(a.n_q_heads, a.batch), dim3(256),
+                     0, stream, a);
+  AEGKV_HIP_TRY(hipGetLastError());
+  return AEGKV_OK;
 }
 
 }  // namespace
@@ -443,18 +613,25 @@ using namespace aegkv;
 extern "C" {
 
 int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_heads,
-                                                     int32_t head_dim, int32_t max_seq_len,
-                                                     int32_t block_size,
-                                                     int32_t blocks_per_split) {
-  if (batch < 0 || n_q_heads <= 0 || head_dim <= 0 || max_seq_len < 0 ||
-      block_size != kBlockSize || blocks_per_split < 0 ||
-      blocks_per_split > kMaxBlocksPerSplit)
+                                                     int32_t n_kv_heads, int32_t head_dim,
+                                                     int32_t max_seq_len, int32_t dtype,
+                                                     int32_t n_workgroups) {
+  if (batch < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads ||
+      n_workgroups < 0 || max_seq_len < 0)
     return AEGKV_ERR_INVALID_ARG;
-  const int bps = blocks_per_split > 0 ? blocks_per_split : kDefaultBlocksPerSplit;
-  const int64_t ms = max_splits_for(max_seq_len, bps);
-  if (ms <= 1) return 0;
-  const int64_t n = (int64_t)batch * n_q_heads * ms;
-  return n * head_dim * (int64_t)sizeof(float) + n * (int64_t)sizeof(float2) + 256;
+  if ((head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+      (dtype != AEGKV_DTYPE_BF16 && dtype != AEGKV_DTYPE_FP16) || n_q_heads / n_kv_heads > 16)
+    return AEGKV_ERR_UNSUPPORTED;
+  if (batch == 0) return 0;
+  const int32_t chunk = std::min(batch, kMaxBatch);
+  if ((int64_t)chunk * (((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize) >= (1ll << 31))
+    return AEGKV_ERR_UNSUPPORTED;
+  int n_wg = 0;
+  const int rc = workgroups_for(n_workgroups, &n_wg);
+  if (rc) return rc > 0 ? AEGKV_ERR_RUNTIME : rc;
+  const int32_t group = n_q_heads / n_kv_heads;
+  const int32_t n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  return workspace_layout(chunk, kHeadsPerGroup * group, head_dim, n_wg, n_groups).total;
 }
 
 int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void* q,
@@ -464,15 +641,14 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
                                  int32_t max_blocks, const int32_t* seq_lens, int32_t batch,
                                  int32_t max_seq_len, int32_t n_q_heads, int32_t n_kv_heads,
                                  int32_t head_dim, int32_t block_size, float scale,
-                                 int32_t dtype, int32_t blocks_per_split, void* workspace,
+                                 int32_t dtype, int32_t n_workgroups, void* workspace,
                                  uint64_t workspace_bytes, aegkv_stream_t stream) {
   if (batch < 0 || max_seq_len < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_blocks < 0 ||
-      n_blocks < 0 || blocks_per_split < 0)
+      n_blocks < 0 || n_workgroups < 0)
     return AEGKV_ERR_INVALID_ARG;
   if (n_q_heads % n_kv_heads) return AEGKV_ERR_INVALID_ARG;
   if (block_size != kBlockSize || (head_dim != 64 && head_dim != 128 && head_dim != 256) ||
-      n_q_heads / n_kv_heads > 16 || (dtype != AEGKV_DTYPE_BF16 && dtype != AEGKV_DTYPE_FP16) ||
-      blocks_per_split > kMaxBlocksPerSplit)
+      n_q_heads / n_kv_heads > 16 || (dtype != AEGKV_DTYPE_BF16 && dtype != AEGKV_DTYPE_FP16))
     return AEGKV_ERR_UNSUPPORTED;
   if (batch == 0) return AEGKV_OK;
   if (!out || !q || !key_cache || !value_cache || !block_tables || !seq_lens || n_blocks == 0)
@@ -481,52 +657,61 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
       ((q_batch_stride * 2) & 15) || ((out_batch_stride * 2) & 15) ||
       ((cache_block_stride * 2) & 15))
     return AEGKV_ERR_MISALIGNED;
-  if (batch > 65535 || n_kv_heads > 65535 * kHeadsPerGroup) return AEGKV_ERR_UNSUPPORTED;
-  const int nblk_max = (max_seq_len + kBlockSize - 1) / kBlockSize;
+  if (n_q_heads > 65535) return AEGKV_ERR_UNSUPPORTED;
+  const int64_t nblk_max = ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize;
   if (nblk_max > max_blocks) return AEGKV_ERR_INVALID_ARG;
-  const int bps = blocks_per_split > 0 ? blocks_per_split : kDefaultBlocksPerSplit;
-  const int ms = max_splits_for(max_seq_len, bps);
-  if (ms > 65535) return AEGKV_ERR_UNSUPPORTED;
+  const int32_t chunk = std::min(batch, kMaxBatch);
+  if ((int64_t)chunk * nblk_max >= (1ll << 31)) return AEGKV_ERR_UNSUPPORTED;
+  int n_wg = 0;
+  int rc = workgroups_for(n_workgroups, &n_wg);
+  if (rc) return rc;
+  const int32_t group = n_q_heads / n_kv_heads;
+  const int32_t n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  const WorkspaceLayout lay =
+      workspace_layout(chunk, kHeadsPerGroup * group, head_dim, n_wg, n_groups);
+  if (!workspace || workspace_bytes < (uint64_t)lay.total) return AEGKV_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return AEGKV_ERR_MISALIGNED;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
   AttnArgs a;
-  a.q = static_cast<const uint16_t*>(q);
-  a.q_bstride = q_batch_stride;
   a.kc = static_cast<const uint16_t*>(key_cache);
   a.vc = static_cast<const uint16_t*>(value_cache);
   a.blk_stride = cache_block_stride;
   a.n_blocks = n_blocks;
-  a.block_tables = block_tables;
   a.max_blocks = max_blocks;
-  a.seq_lens = seq_lens;
   a.n_q_heads = n_q_heads;
   a.n_kv_heads = n_kv_heads;
-  a.group = n_q_heads / n_kv_heads;
+  a.group = group;
+  a.hpg = kHeadsPerGroup * group;
+  a.n_groups = n_groups;
+  a.n_wg = n_wg;
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.bps = bps;
-  a.max_splits = ms;
   a.max_seq_len = max_seq_len;
-  a.out = static_cast<uint16_t*>(out);
+  a.q_bstride = q_batch_stride;
   a.out_bstride = out_batch_stride;
-  a.part_o = nullptr;
-  a.part_ml = nullptr;
-  if (ms > 1) {
-    const int64_t need = aegkv_paged_decode_attention_workspace_size(
-        batch, n_q_heads, head_dim, max_seq_len, block_size, bps);
-    if (!workspace || workspace_bytes < (uint64_t)need) return AEGKV_ERR_WORKSPACE;
-    if (!aligned16(workspace)) return AEGKV_ERR_MISALIGNED;
-    const int64_t n = (int64_t)batch * n_q_heads * ms;
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = reinterpret_cast<float2*>(static_cast<float*>(workspace) + n * head_dim);
-  }
+  a.cum = reinterpret_cast<int32_t*>(ws);
+  a.part_ml = reinterpret_cast<float2*>(ws + lay.cum_bytes);
+  a.part_o = reinterpret_cast<float*>(ws + lay.cum_bytes + lay.ml_bytes);
   hipStream_t st = (hipStream_t)stream;
   const bool bf = dtype == AEGKV_DTYPE_BF16;
-  switch (head_dim) {
-    case 64: return bf ? launch_attention<AEGKV_DTYPE_BF16, 64>(a, batch, st)
-                       : launch_attention<AEGKV_DTYPE_FP16, 64>(a, batch, st);
-    case 128: return bf ? launch_attention<AEGKV_DTYPE_BF16, 128>(a, batch, st)
-                        : launch_attention<AEGKV_DTYPE_FP16, 128>(a, batch, st);
-    default: return bf ? launch_attention<AEGKV_DTYPE_BF16, 256>(a, batch, st)
-                       : launch_attention<AEGKV_DTYPE_FP16, 256>(a, batch, st);
+  // Batches above kMaxBatch run as consecutive launches of kMaxBatch sequences
+  // that share the workspace (stream order keeps them apart).
+  for (int32_t c = 0; c < batch; c += kMaxBatch) {
+    a.batch = std::min(kMaxBatch, batch - c);
+    a.q = static_cast<const uint16_t*>(q) + (int64_t)c * q_batch_stride;
+    a.out = static_cast<uint16_t*>(out) + (int64_t)c * out_batch_stride;
+    a.block_tables = block_tables + (int64_t)c * max_blocks;
+    a.seq_lens = seq_lens + c;
+    switch (head_dim) {
+      case 64: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 64>(a, st)
+                       : launch_attention<AEGKV_DTYPE_FP16, 64>(a, st); break;
+      case 128: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 128>(a, st)
+                        : launch_attention<AEGKV_DTYPE_FP16, 128>(a, st); break;
+      default: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 256>(a, st)
+                       : launch_attention<AEGKV_DTYPE_FP16, 256>(a, st); break;
+    }
+    if (rc) return rc;
   }
+  return AEGKV_OK;
 }
 
 }  // extern "C"

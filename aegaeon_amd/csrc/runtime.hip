@@ -146,6 +146,7 @@ const char* aegkv_strerror(int code) {
     case AEGKV_ERR_DUPLICATE: return "aegkv: duplicate destination block id";
     case AEGKV_ERR_UNSUPPORTED: return "aegkv: unsupported shape or dtype";
     case AEGKV_ERR_WORKSPACE: return "aegkv: workspace or staging buffer too small";
+    case AEGKV_ERR_RUNTIME: return "aegkv: a HIP runtime query failed while sizing the call";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);

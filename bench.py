@@ -186,12 +186,13 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
     view = cache.permute(1, 2, 0, 3, 4, 5)
     scale = 1.0 / math.sqrt(g.head_dim)
     outs = torch.empty_like(q)
-    ws = A.attention_workspace(wb.batch, g.n_q_heads, g.head_dim, max_len, args.bps, device=dev)
+    ws = A.attention_workspace(wb.batch, g.n_q_heads, g.n_kv_heads, g.head_dim, max_len,
+                               torch.bfloat16, args.nwg, device=dev)
 
     def layer_call(i):
         layer = i % g.n_layers
         A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], bt, sl, scale,
-                                 max_len, out=outs[layer], blocks_per_split=args.bps,
+                                 max_len, out=outs[layer], n_workgroups=args.nwg,
                                  workspace=ws)
 
     for i in range(g.n_layers):
@@ -314,7 +315,8 @@ def bench_defrag(args, timer):
     max_len = int(wb.seq_lens.max())
     view = typed.permute(1, 2, 0, 3, 4, 5)
     out = torch.empty_like(q)
-    ws = A.attention_workspace(wb.batch, g.n_q_heads, g.head_dim, max_len, args.bps, device=dev)
+    ws = A.attention_workspace(wb.batch, g.n_q_heads, g.n_kv_heads, g.head_dim, max_len,
+                               torch.bfloat16, args.nwg, device=dev)
     scale = 1.0 / math.sqrt(g.head_dim)
 
     def app(i):
@@ -323,7 +325,7 @@ def bench_defrag(args, timer):
     def attn(i):
         layer = i % g.n_layers
         A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], bt, sl, scale,
-                                 max_len, out=out[layer], blocks_per_split=args.bps,
+                                 max_len, out=out[layer], n_workgroups=args.nwg,
                                  workspace=ws)
 
     app(0)
@@ -431,7 +433,8 @@ def main(argv=None):
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--bps", type=int, default=0, help="attention blocks per split (0 = default)")
+    p.add_argument("--nwg", type=int, default=0,
+                   help="attention workgroups (0 = the device's resident capacity)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--swap-seqs", type=int, default=32)

@@ -47,6 +47,7 @@ typedef void* aegkv_stream_t; /* hipStream_t */
 #define AEGKV_ERR_DUPLICATE (-5)     /* a destination block id appears twice     */
 #define AEGKV_ERR_UNSUPPORTED (-6)   /* shape/dtype the kernels do not cover     */
 #define AEGKV_ERR_WORKSPACE (-7)     /* workspace/staging smaller than required  */
+#define AEGKV_ERR_RUNTIME (-8)       /* a HIP runtime query failed while sizing  */
 
 /* dtype codes for the K/V and query elements */
 #define AEGKV_DTYPE_BF16 0
@@ -164,22 +165,27 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
  *   key_cache/value_cache: [N][block_size][n_kv_heads][head_dim] per block with
  *     block stride cache_block_stride (the reference's permuted per-layer view).
  *   block_tables [batch][max_blocks] int32, seq_lens [batch] int32: DEVICE arrays.
- *   max_seq_len: host upper bound of seq_lens (sizes the split-KV grid); device
- *     lengths above it are clamped to it, so a wrong bound never reads or writes
- *     out of bounds.
- *   blocks_per_split: KV blocks per work item, 1..64 (0 = library default, 16).
- *   workspace: DEVICE scratch for split-KV partials of
- *     aegkv_paged_decode_attention_workspace_size(...) bytes.
- * Supported: block_size 16, head_dim 64/128/256, n_q_heads/n_kv_heads <= 16,
- * blocks_per_split <= 64 (AEGKV_ERR_UNSUPPORTED otherwise).
- * seq_lens[b] == 0 yields zeros.  A block id outside [0, n_blocks) is never
- * dereferenced: its tokens are masked out of the softmax.  n_blocks must be >= 1
- * (AEGKV_ERR_INVALID_ARG otherwise). */
+ *   max_seq_len: host upper bound of seq_lens; device lengths above it are
+ *     clamped to it, so a wrong bound never reads or writes out of bounds.
+ *   n_workgroups: workgroups that share the batch's KV blocks in equal
+ *     contiguous ranges (0 = the device's resident capacity, the fast choice;
+ *     any positive count gives the same result).
+ *   workspace: DEVICE scratch of
+ *     aegkv_paged_decode_attention_workspace_size(...) bytes (same batch, heads,
+ *     head_dim, max_seq_len, dtype, n_workgroups and device); it holds the
+ *     batch's block prefix sums and the partials of sequences that several
+ *     workgroups share.  Its contents need no initialisation.
+ * Supported: block_size 16, head_dim 64/128/256, n_q_heads/n_kv_heads <= 16
+ * (AEGKV_ERR_UNSUPPORTED otherwise).  Batches above 2048 sequences run as
+ * consecutive launches of 2048.  seq_lens[b] == 0 yields zeros.  A block id
+ * outside [0, n_blocks) is never dereferenced: its tokens are masked out of
+ * the softmax.  n_blocks must be >= 1 (AEGKV_ERR_INVALID_ARG otherwise).
+ * The size query returns bytes, or a negative status (AEGKV_ERR_RUNTIME when
+ * the device query behind n_workgroups = 0 failed). */
 int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_heads,
-                                                     int32_t head_dim,
-                                                     int32_t max_seq_len,
-                                                     int32_t block_size,
-                                                     int32_t blocks_per_split);
+                                                     int32_t n_kv_heads, int32_t head_dim,
+                                                     int32_t max_seq_len, int32_t dtype,
+                                                     int32_t n_workgroups);
 int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void* q,
                                  int64_t q_batch_stride, const void* key_cache,
                                  const void* value_cache, int64_t cache_block_stride,
@@ -188,7 +194,7 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
                                  int32_t batch, int32_t max_seq_len, int32_t n_q_heads,
                                  int32_t n_kv_heads, int32_t head_dim,
                                  int32_t block_size, float scale, int32_t dtype,
-                                 int32_t blocks_per_split, void* workspace,
+                                 int32_t n_workgroups, void* workspace,
                                  uint64_t workspace_bytes, aegkv_stream_t stream);
 
 #ifdef __cplusplus

@@ -115,17 +115,31 @@ def test_append_and_gather_argument_checks(lib):
 def test_attention_argument_checks_and_workspace_size(lib):
     raw, p = _buf(1 << 16)
     ws = lib.aegkv_paged_decode_attention_workspace_size
-    assert ws(4, 28, 128, 0, 16, 0) == 0
-    assert ws(4, 28, 128, 100, 12, 0) == INVALID
-    big = ws(128, 28, 128, 8192, 16, 0)
-    assert big > 0 and big == ws(128, 28, 128, 8192, 16, 0)
-    assert ws(128, 28, 128, 8192, 16, 0) >= ws(128, 28, 128, 4096, 16, 0)
+    # (batch, Hq, Hkv, D, max_seq_len, dtype, n_workgroups); an explicit
+    # workgroup count sizes the workspace without a device query
+    assert ws(0, 28, 4, 128, 4096, 0, 8) == 0
+    assert ws(4, 28, 4, 100, 4096, 0, 8) == UNSUP
+    assert ws(4, 30, 4, 128, 4096, 0, 8) == INVALID
+    assert ws(4, 28, 4, 128, 4096, 9, 8) == UNSUP
+    assert ws(4, 28, 4, 128, 4096, 0, -1) == INVALID
+    # prefix sums (batch + 1 int32, 256-byte aligned), then (n_wg + groups*batch)
+    # slots of hpg = 4 * 7 query heads: float2 (m, l) and D floats each
+    slots = 8 + 1 * 4
+    want = 256 + -(-slots * 28 * 8 // 256) * 256 + -(-slots * 28 * 128 * 4 // 256) * 256
+    assert ws(4, 28, 4, 128, 4096, 0, 8) == want
+    assert ws(4, 28, 4, 128, 4096, 0, 16) > want
+    # Llama-shaped 40/40: ten groups of four kv heads, one query head each
+    slots = 8 + 10 * 4
+    assert ws(4, 40, 40, 128, 4096, 1, 8) == (
+        256 + -(-slots * 4 * 8 // 256) * 256 + -(-slots * 4 * 128 * 4 // 256) * 256)
+    # batches above 2048 are launched in chunks of 2048 sharing one workspace
+    assert ws(5000, 28, 4, 128, 4096, 0, 8) == ws(2048, 28, 4, 128, 4096, 0, 8)
 
     def attn(Hq=28, Hkv=4, D=128, bs=16, dtype=0, max_len=64, max_blocks=4, wsp=None, wsb=0,
-             bps=0, q=p):
+             nwg=0, q=p):
         return lib.aegkv_paged_decode_attention(p, Hq * D, q, Hq * D, p, p, 16 * Hkv * D, 8, p,
                                                 max_blocks, p, 2, max_len, Hq, Hkv, D, bs, 0.1,
-                                                dtype, bps, wsp, wsb, None)
+                                                dtype, nwg, wsp, wsb, None)
 
     assert attn(Hq=30) == INVALID
     assert attn(D=96) == UNSUP
@@ -133,9 +147,10 @@ def test_attention_argument_checks_and_workspace_size(lib):
     assert attn(dtype=7) == UNSUP
     assert attn(Hq=34, Hkv=2) == UNSUP  # group of 17 > 16
     assert attn(max_len=100) == INVALID  # needs 7 blocks, table has 4
-    need = ws(2, 28, 128, 4096, 16, 1)
+    assert attn(nwg=-1) == INVALID
+    need = ws(2, 28, 4, 128, 4096, 0, 1)
     assert need > 0
-    assert attn(max_len=4096, max_blocks=256, bps=1) == WS
-    assert attn(max_len=4096, max_blocks=256, bps=1, wsp=p, wsb=need - 1) == WS
+    assert attn(max_len=4096, max_blocks=256, nwg=1) == WS
+    assert attn(max_len=4096, max_blocks=256, nwg=1, wsp=p, wsb=need - 1) == WS
     raw2, mis = _buf(64, misalign=4)
     assert attn(q=mis) == MISALIGNED

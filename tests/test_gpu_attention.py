@@ -52,7 +52,7 @@ def _check(out_bits, ref, dtype):
     return err
 
 
-def _run(device, lens, Hq, Hkv, D, dtype, bps=0, seed=0, kc_override=None):
+def _run(device, lens, Hq, Hkv, D, dtype, nwg=0, seed=0, kc_override=None):
     rng = np.random.default_rng(seed)
     lens, tables, padded, q, kc, vc = _setup(rng, lens, Hq, Hkv, D, dtype)
     if kc_override is not None:
@@ -62,7 +62,7 @@ def _run(device, lens, Hq, Hkv, D, dtype, bps=0, seed=0, kc_override=None):
         to_device_bits(q, dtype, device), to_device_bits(kc, dtype, device),
         to_device_bits(vc, dtype, device), torch.from_numpy(padded).to(device),
         torch.from_numpy(lens.astype(np.int32)).to(device), scale, int(lens.max()),
-        blocks_per_split=bps)
+        n_workgroups=nwg)
     ref = ko.paged_decode_attention(ko.bits_to_float(q, dtype), ko.bits_to_float(kc, dtype),
                                     ko.bits_to_float(vc, dtype), padded, lens, scale)
     return to_bits(out), ref, (lens, tables, padded, q, kc, vc)
@@ -70,12 +70,23 @@ def _run(device, lens, Hq, Hkv, D, dtype, bps=0, seed=0, kc_override=None):
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 @pytest.mark.parametrize("Hq,Hkv,D", [(28, 4, 128), (32, 4, 128), (8, 8, 128), (16, 1, 64),
-                                      (6, 2, 256)])
-@pytest.mark.parametrize("bps", [0, 1, 3, 64])
-def test_matches_fp64_textbook(device, dtype, Hq, Hkv, D, bps):
-    lens = [1, 15, 16, 17, 31, 64, 200, 517]
-    out, ref, _ = _run(device, lens, Hq, Hkv, D, dtype, bps=bps, seed=Hq * 1000 + D + bps)
+                                      (6, 2, 256), (12, 6, 128), (40, 40, 128)])
+@pytest.mark.parametrize("nwg", [0, 1, 3, 64, 1000])
+def test_matches_fp64_textbook(device, dtype, Hq, Hkv, D, nwg):
+    """Every workgroup count partitions the same blocks differently (one
+    workgroup walking all sequences; pieces of a few blocks; more workgroups
+    than blocks); the result must not depend on it."""
+    lens = [1, 15, 16, 17, 31, 64, 200, 517, 0, 1100]
+    out, ref, _ = _run(device, lens, Hq, Hkv, D, dtype, nwg=nwg, seed=Hq * 1000 + D + nwg)
     _check(out, ref, dtype)
+
+
+def test_batch_above_one_launch(device):
+    """2500 sequences run as launches of 2048 and 452 sharing one workspace."""
+    rng = np.random.default_rng(11)
+    lens = rng.integers(0, 70, size=2500)
+    out, ref, _ = _run(device, lens, 8, 2, 64, "bf16", seed=11)
+    _check(out, ref, "bf16")
 
 
 def test_len_one_returns_v0_exactly(device):
