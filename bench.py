@@ -14,11 +14,12 @@ cannot serve the inputs from a previous step: every step reads and writes HBM.
 Timing.  The host enqueues a launch in ~10 us of Python; a 8 us kernel would
 then measure the host.  Each timed region therefore starts behind a bounded
 spin kernel (torch.cuda._sleep) that holds the stream while the host enqueues
-all K launches; the GPU then runs them back to back:
-  * ms_per_step: HIP events at both ends of the K launches, divided by K
-    (device time per step including the gaps between launches);
-  * roofline.achieved: algorithmic bytes over the mean of per-launch HIP event
-    pairs (device duration of one launch), on the stream the kernels run on.
+all K launches; the GPU then runs them back to back.  HIP events recorded on
+the stream the kernels run on (torch's current stream, which every op of the
+package launches on) bracket the K launches; their elapsed time over K is the
+average device duration of one step, the quantity rocprofv3 reports per
+kernel (back-to-back launches leave no gap between kernels).  ``value`` and
+``roofline.achieved`` are the algorithmic bytes over that duration.
 torch.cuda.synchronize() brackets every timed region.
 
 Secondary lines (``ops``): the per-layer launch pattern of vLLM; paged decode
@@ -87,30 +88,18 @@ class Timer:
         torch.cuda._sleep(int(hold_ms * self.cycles_per_ms))
 
     def run(self, fn, steps: int):
-        """Returns (ms per step over the whole region, mean per-launch ms, wall s)."""
+        """Returns (device ms per call over the held region, wall s)."""
         torch = self.torch
-        Ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         self._hold(fn, steps)
-        start, end = Ev(), Ev()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for i in range(steps):
             fn(i)
         end.record()
         torch.cuda.synchronize()
-        region_ms = start.elapsed_time(end) / steps
-        wall = time.perf_counter() - t0
-        # per-launch event pairs
-        pairs = [(Ev(), Ev()) for _ in range(steps)]
-        self._hold(fn, 2 * steps)
-        for i, (a, b) in enumerate(pairs):
-            a.record()
-            fn(i)
-            b.record()
-        torch.cuda.synchronize()
-        per = [a.elapsed_time(b) for a, b in pairs]
-        return region_ms, float(np.mean(per)), wall
+        return start.elapsed_time(end) / steps, time.perf_counter() - t0
 
 
 # ----------------------------------------------------------------------------- append
@@ -147,15 +136,14 @@ def bench_append(args, timer):
     for i in range(args.warmup):
         cold(i)
     torch.cuda.synchronize()
-    region_ms, launch_ms, wall = timer.run(cold, args.steps)
-    hot_region, hot_launch, _ = timer.run(hot, args.steps)
-    pl_region, pl_launch, _ = timer.run(per_layer, max(4, args.steps // 8))
+    region_ms, wall = timer.run(cold, args.steps)
+    hot_ms, _ = timer.run(hot, args.steps)
+    pl_ms, _ = timer.run(per_layer, max(4, args.steps // 8))
     nbytes = wb.append_bytes()
     del cache, keys, vals
     torch.cuda.empty_cache()
-    return {"wb": wb, "bytes": nbytes, "region_ms": region_ms, "launch_ms": launch_ms,
-            "wall_s": wall, "hot_launch_ms": hot_launch, "hot_region_ms": hot_region,
-            "per_layer_step_ms": pl_region}
+    return {"wb": wb, "bytes": nbytes, "ms": region_ms, "wall_s": wall, "hot_ms": hot_ms,
+            "per_layer_step_ms": pl_ms}
 
 
 # -------------------------------------------------------------------------- attention
@@ -199,12 +187,12 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
         layer_call(i)
     torch.cuda.synchronize()
     steps = max(g.n_layers, (args.steps // g.n_layers) * g.n_layers)
-    region_ms, launch_ms, _ = timer.run(layer_call, steps)
+    region_ms, _ = timer.run(layer_call, steps)
     nbytes = wb.attention_bytes()
     del cache
     torch.cuda.empty_cache()
     return {"label": label, "wb": wb, "bytes_per_layer": nbytes, "us_per_layer": region_ms * 1e3,
-            "launch_us": launch_ms * 1e3}
+            }
 
 
 # ------------------------------------------------------------------------ pack / swap
@@ -234,8 +222,8 @@ def bench_pack(args, timer):
     scatter(0)
     torch.cuda.synchronize()
     steps = max(2, args.steps // 40)
-    p_region, p_launch, _ = timer.run(pack, steps)
-    s_region, s_launch, _ = timer.run(scatter, steps)
+    p_ms, _ = timer.run(pack, steps)
+    s_ms, _ = timer.run(scatter, steps)
     nbytes = wl.pack_bytes()
     # PCIe leg on a sample: D2H of packed blocks into pinned host, then H2D back
     n_s = min(args.pcie_blocks, wl.n_blocks)
@@ -252,8 +240,8 @@ def bench_pack(args, timer):
     h2d = n_s * bb / (e[1].elapsed_time(e[2]) * 1e-3) / 1e9
     del pool, staging, host
     torch.cuda.empty_cache()
-    return {"wl": wl, "bytes": nbytes, "pack_ms": p_launch, "scatter_ms": s_launch,
-            "pack_region_ms": p_region, "pcie_blocks": n_s, "d2h_gbs": d2h, "h2d_gbs": h2d}
+    return {"wl": wl, "bytes": nbytes, "pack_ms": p_ms, "scatter_ms": s_ms,
+            "pcie_blocks": n_s, "d2h_gbs": d2h, "h2d_gbs": h2d}
 
 
 # ------------------------------------------------------------- unified pool + defrag
@@ -290,7 +278,7 @@ def bench_defrag(args, timer):
     defrag(1)
     torch.cuda.synchronize()
     steps = max(2, args.steps // 20)
-    region_ms, launch_ms, _ = timer.run(defrag, steps)
+    defrag_ms, _ = timer.run(defrag, steps)
     for name, (s, d) in snapshot.items():
         moved_bytes += 2 * len(s) * wl.geometries[name].block_bytes + 16 * len(s)
     n_moved = {n: int(len(s)) for n, (s, _) in snapshot.items()}
@@ -331,13 +319,13 @@ def bench_defrag(args, timer):
     app(0)
     attn(0)
     torch.cuda.synchronize()
-    a_region, a_launch, _ = timer.run(app, max(4, args.steps // 4))
-    t_region, t_launch, _ = timer.run(attn, g.n_layers * max(1, args.steps // 100))
+    a_ms, _ = timer.run(app, max(4, args.steps // 4))
+    t_ms, _ = timer.run(attn, g.n_layers * max(1, args.steps // 100))
     del pool, typed
     torch.cuda.empty_cache()
-    return {"defrag_ms": launch_ms, "defrag_bytes": moved_bytes, "moved_blocks": n_moved,
-            "yi_append_ms": a_launch, "yi_append_bytes": wb.append_bytes(),
-            "yi_attn_us_per_layer": t_region * 1e3, "yi_attn_bytes": wb.attention_bytes(),
+    return {"defrag_ms": defrag_ms, "defrag_bytes": moved_bytes, "moved_blocks": n_moved,
+            "yi_append_ms": a_ms, "yi_append_bytes": wb.append_bytes(),
+            "yi_attn_us_per_layer": t_ms * 1e3, "yi_attn_bytes": wb.attention_bytes(),
             "yi_batch": wb.batch}
 
 
@@ -365,11 +353,37 @@ def bench_gather(args, timer):
 
     gather(0)
     torch.cuda.synchronize()
-    region_ms, launch_ms, _ = timer.run(gather, max(g.n_layers, args.steps // 4))
+    region_ms, _ = timer.run(gather, max(g.n_layers, args.steps // 4))
     nbytes = 2 * 2 * total * g.row_elems * 2 + 4 * sum(-(-int(x) // 16) for x in sl_np)
     del cache
     torch.cuda.empty_cache()
-    return {"bytes": nbytes, "launch_ms": launch_ms, "region_ms": region_ms}
+    return {"bytes": nbytes, "ms": region_ms}
+
+
+# ------------------------------------------------------------------ copy calibration
+CALIB_BLOCKS, CALIB_BLOCK_BYTES = 256, 1 << 20
+
+
+def bench_calib(args, timer):
+    """A plain copy of known size for scaling the HBM byte counters: pack
+    blocks 0..255 of 1 MiB (contiguous) into a staging buffer, i.e. read
+    256 MiB and write 256 MiB with the block-copy kernel."""
+    import torch
+    from aegaeon_amd import ops
+    dev = torch.device("cuda", 0)
+    pool = torch.ones((4 * CALIB_BLOCKS, CALIB_BLOCK_BYTES), dtype=torch.uint8, device=dev)
+    out = torch.empty((CALIB_BLOCKS, CALIB_BLOCK_BYTES), dtype=torch.uint8, device=dev)
+    ids = np.arange(CALIB_BLOCKS, dtype=np.int64)
+
+    def copy(i):
+        ops.pack_blocks(pool, ids + CALIB_BLOCKS * (i % 4), out=out)
+
+    copy(0)
+    torch.cuda.synchronize()
+    ms, _ = timer.run(copy, 8)
+    del pool, out
+    torch.cuda.empty_cache()
+    return {"bytes": 2 * CALIB_BLOCKS * CALIB_BLOCK_BYTES, "ms": ms}
 
 
 # ---------------------------------------------------------------------- CPU baseline
@@ -434,13 +448,13 @@ def main(argv=None):
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--nwg", type=int, default=0,
-                   help="attention workgroups (0 = the device's resident capacity)")
+                   help="attention workgroups (0 = one per CU)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--swap-seqs", type=int, default=32)
     p.add_argument("--pcie-blocks", type=int, default=64)
     p.add_argument("--only", default="all",
-                   help="comma list of append,attention,pack,defrag,gather or 'all'")
+                   help="comma list of append,attention,pack,defrag,gather,calib or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU and "
@@ -455,12 +469,13 @@ def main(argv=None):
     torch.cuda.set_device(0)
     log(f"device: {torch.cuda.get_device_name(0)}")
     only = set(args.only.split(",")) if args.only != "all" else \
-        {"append", "attention", "pack", "defrag", "gather"}
+        {"append", "attention", "pack", "defrag", "gather", "calib"}
     timer = Timer()
     log(f"spin calibration: {timer.cycles_per_ms:.0f} cycles/ms")
     res = {}
     for name, fn in (("append", bench_append), ("attention", bench_attention),
-                     ("gather", bench_gather), ("pack", bench_pack), ("defrag", bench_defrag)):
+                     ("gather", bench_gather), ("pack", bench_pack), ("defrag", bench_defrag),
+                     ("calib", bench_calib)):
         if name in only:
             t0 = time.perf_counter()
             res[name] = fn(args, timer)
@@ -478,21 +493,20 @@ def main(argv=None):
     ops_out = {}
     if "append" in res:
         a = res["append"]
-        value = a["bytes"] / (a["region_ms"] * 1e-3) / 1e9
-        achieved = a["bytes"] / (a["launch_ms"] * 1e-3) / 1e9
+        value = a["bytes"] / (a["ms"] * 1e-3) / 1e9
         line.update({
-            "value": round(value, 1), "ms_per_step": round(a["region_ms"], 6),
+            "value": round(value, 1), "ms_per_step": round(a["ms"], 6),
             "config": {"workload": "Qwen2.5-7B-shaped decode-step KV append, all 28 layers in "
                                    "one launch, 256 sequences (lognormal mean 600), bf16",
                        "layers": 28, "kv_heads": 4, "head_dim": 128, "block_size": 16,
                        "batch": a["wb"].batch, "pool_blocks": a["wb"].n_pool_blocks,
                        "bytes_per_step": a["bytes"], "rotated_steps": ROTATE_STEPS},
-            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
                          "traffic": _traffic()},
         })
-        ops_out["append_kernel_us"] = round(a["launch_ms"] * 1e3, 2)
-        ops_out["append_same_inputs_every_step_us"] = round(a["hot_launch_ms"] * 1e3, 2)
+        ops_out["append_kernel_us"] = round(a["ms"] * 1e3, 2)
+        ops_out["append_same_inputs_every_step_us"] = round(a["hot_ms"] * 1e3, 2)
         ops_out["append_per_layer_28_launches_us"] = round(a["per_layer_step_ms"] * 1e3, 2)
     if "attention" in res:
         t = res["attention"]
@@ -501,7 +515,6 @@ def main(argv=None):
             "workload": "Qwen2.5-7B GQA 28/4, D 128, bf16, 128 seqs, lognormal mean 1500 "
                         "(sum len 189059), 28 layers back to back",
             "us_per_layer": round(t["us_per_layer"], 2),
-            "us_per_call_events": round(t["launch_us"], 2),
             "bytes_per_layer": t["bytes_per_layer"], "GB/s": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         if "value" not in line:
@@ -509,10 +522,10 @@ def main(argv=None):
                          "higher_is_better": False})
     if "gather" in res:
         gt = res["gather"]
-        gbs = gt["bytes"] / (gt["launch_ms"] * 1e-3) / 1e9
+        gbs = gt["bytes"] / (gt["ms"] * 1e-3) / 1e9
         ops_out["gather_tokens_one_layer"] = {
             "workload": "Qwen2.5-7B append batch, 256 seqs, one layer K+V",
-            "us": round(gt["launch_ms"] * 1e3, 2), "bytes": gt["bytes"], "GB/s": round(gbs, 1),
+            "us": round(gt["ms"] * 1e3, 2), "bytes": gt["bytes"], "GB/s": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     if "pack" in res:
         pk = res["pack"]
@@ -538,6 +551,13 @@ def main(argv=None):
             "yi_append_us": round(d["yi_append_ms"] * 1e3, 2), "yi_append_GB/s": round(ag, 1),
             "yi_attention_us_per_layer": round(d["yi_attn_us_per_layer"], 2),
             "yi_attention_GB/s": round(tg, 1), "yi_attention_frac_hbm": round(tg / HBM_PEAK_GBS, 4)}
+    if "calib" in res:
+        c = res["calib"]
+        cg = c["bytes"] / (c["ms"] * 1e-3) / 1e9
+        ops_out["copy_calibration"] = {
+            "workload": "pack of 256 contiguous 1 MiB blocks (256 MiB read + 256 MiB write)",
+            "us": round(c["ms"] * 1e3, 2), "bytes": c["bytes"], "GB/s": round(cg, 1),
+            "frac_hbm": round(cg / HBM_PEAK_GBS, 4)}
     line["ops"] = ops_out
     if cpu is not None:
         line["cpu_baseline"] = cpu
