@@ -3,10 +3,14 @@
 // (aegaeon/ops/swap.cu:25-59).
 //
 // One kernel serves every device-side move.  A block of block_bytes is cut into
-// 16 KiB tiles; a 256-thread workgroup moves one tile per iteration with four
-// dwordx4 (16 B) loads per lane issued before the four stores, so each wave
-// keeps 4 KiB in flight and every access is a fully coalesced 1 KiB wave row.
-// The grid is persistent (a few workgroups per CU) and strides over tiles.
+// 16 KiB tiles and the tiles of all blocks are laid end to end, then grouped
+// into chunks of chunk_tiles consecutive tiles; a persistent grid of G
+// workgroups deals the chunks round-robin (workgroup w copies chunks w, w + G,
+// ...), one tile per iteration.  Per tile, each lane issues four non-temporal
+// dwordx4 loads before the four stores (4 KiB in flight per wave, every
+// access a fully coalesced 1 KiB wave row).  The block ids of a workgroup's
+// next tile are loaded together with the current tile's data, so no tile waits
+// on an id load in front of its own loads.
 #include <algorithm>
 #include <numeric>
 
@@ -20,17 +24,35 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kCopyThreads = 256;
 constexpr int kCopyUnroll = 4;
 constexpr uint64_t kTileBytes = (uint64_t)kCopyThreads * 16 * kCopyUnroll;  // 16 KiB
+constexpr int kCopyWorkgroupsPerCu = 32;  // measured best of 2..32 with chunks 1..64 tiles
+constexpr int kCopyChunkTiles = 1;  // 0 = one contiguous range per workgroup
 
 __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
     const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
     const int64_t* __restrict__ src_ids, const int64_t* __restrict__ dst_ids,
-    uint64_t block_bytes, uint32_t tiles_per_block, uint64_t n_tiles) {
-  for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-    const uint64_t i = tile / tiles_per_block;
-    const uint64_t t = tile - i * tiles_per_block;
-    const int64_t s = src_ids ? src_ids[i] : (int64_t)i;
-    const int64_t d = dst_ids ? dst_ids[i] : (int64_t)i;
-    const uint64_t base = t * kTileBytes;
+    uint64_t block_bytes, uint32_t tiles_per_block, uint64_t n_tiles, uint64_t chunk_tiles) {
+  // every value below is uniform over the workgroup
+  const uint64_t stride = (uint64_t)gridDim.x * chunk_tiles;  // tiles between chunk starts
+  uint64_t tile = (uint64_t)blockIdx.x * chunk_tiles;
+  if (tile >= n_tiles) return;
+  uint64_t chunk_end = min(tile + chunk_tiles, n_tiles);
+  uint64_t i = tile / tiles_per_block;  // block index of the current tile
+  int64_t s = src_ids ? src_ids[i] : (int64_t)i;
+  int64_t d = dst_ids ? dst_ids[i] : (int64_t)i;
+  while (true) {
+    uint64_t next = tile + 1, next_end = chunk_end;
+    if (next >= chunk_end) {  // first tile of this workgroup's next chunk
+      next = chunk_end - chunk_tiles + stride;
+      next_end = min(next + chunk_tiles, n_tiles);
+    }
+    const bool more = next < n_tiles;
+    const uint64_t ni = more ? next / tiles_per_block : i;
+    int64_t ns = s, nd = d;
+    if (ni != i) {
+      ns = src_ids ? src_ids[ni] : (int64_t)ni;
+      nd = dst_ids ? dst_ids[ni] : (int64_t)ni;
+    }
+    const uint64_t base = (tile - i * tiles_per_block) * kTileBytes;
     const uint64_t rem = block_bytes - base;  // bytes of this block from the tile start
     const u32x4* sp = reinterpret_cast<const u32x4*>(src + (uint64_t)s * block_bytes + base);
     u32x4* dp = reinterpret_cast<u32x4*>(dst + (uint64_t)d * block_bytes + base);
@@ -45,6 +67,12 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
       const uint32_t c = k * kCopyThreads + threadIdx.x;
       if ((uint64_t)c * 16 < rem) __builtin_nontemporal_store(r[k], dp + c);
     }
+    if (!more) break;
+    tile = next;
+    chunk_end = next_end;
+    i = ni;
+    s = ns;
+    d = nd;
   }
 }
 
@@ -56,12 +84,15 @@ int launch_copy_blocks(const DeviceState* ds, const void* src, void* dst,
   if (n <= 0) return AEGKV_OK;
   const uint64_t tiles_per_block = (block_bytes + kTileBytes - 1) / kTileBytes;
   const uint64_t n_tiles = tiles_per_block * (uint64_t)n;
-  const uint64_t max_grid = (uint64_t)std::max(ds->num_cu, 1) * 8;
-  const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, max_grid);
+  const uint64_t max_grid = (uint64_t)std::max(ds->num_cu, 1) * kCopyWorkgroupsPerCu;
+  const uint64_t chunk = kCopyChunkTiles > 0 ? (uint64_t)kCopyChunkTiles
+                                             : (n_tiles + max_grid - 1) / max_grid;
+  const uint64_t n_chunks = (n_tiles + chunk - 1) / chunk;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>(n_chunks, max_grid);
   hipLaunchKernelGGL(copy_blocks_kernel, dim3(grid), dim3(kCopyThreads), 0, stream,
                      static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst),
                      src_ids_dev, dst_ids_dev, block_bytes, (uint32_t)tiles_per_block,
-                     n_tiles);
+                     n_tiles, chunk);
   AEGKV_HIP_TRY(hipGetLastError());
   return AEGKV_OK;
 }
