@@ -14,7 +14,8 @@ All of them enqueue hand-written gfx950 kernels on the current torch stream.
 from __future__ import annotations
 
 import math
-from typing import Optional, Sequence, Tuple
+import threading
+from typing import Dict, Optional, Sequence, Tuple
 
 import torch
 
@@ -161,12 +162,28 @@ def attention_workspace(batch: int, n_q_heads: int, n_kv_heads: int, head_dim: i
                         max_seq_len: int, dtype: torch.dtype = torch.bfloat16,
                         n_workgroups: int = 0, device=None) -> Optional[torch.Tensor]:
     """A device workspace large enough for every call of these sizes (None
-    when the call needs none).  Reusable across calls on one stream."""
+    when the call needs none); reusable by consecutive calls on one stream,
+    calls that may overlap (other streams) need their own."""
     n = attention_workspace_bytes(batch, n_q_heads, n_kv_heads, head_dim, max_seq_len, dtype,
                                   n_workgroups, device)
     if n == 0:
         return None
     return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+# Workspaces kept per (device, stream) for calls that bring none.
+_workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+_ws_lock = threading.Lock()
+
+
+def _cached_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+        return ws
 
 
 def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
@@ -176,8 +193,10 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
                            workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Paged GQA decode attention: ``q [B, Hq, D]`` against per-layer cache
     views ``[N, 16, Hkv, D]``; returns ``out [B, Hq, D]`` in q's dtype.
-    ``n_workgroups`` = 0 spreads the batch over the device's resident
-    workgroups; a positive count forces that many (same result)."""
+    ``n_workgroups`` = 0 spreads the batch over one workgroup per CU; a
+    positive count forces that many (same result).  ``workspace``: from
+    :func:`attention_workspace` (reusable on one stream); by default a cached
+    one per (device, stream)."""
     if q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.size(2) or not q.is_cuda:
         raise ValueError("q must be a GPU tensor [B, Hq, D] with dense heads")
     _check_cache_view(key_cache, "key_cache")
@@ -200,8 +219,11 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
         return out
     ws_bytes = attention_workspace_bytes(B, Hq, Hkv, D, max_seq_len, q.dtype, n_workgroups,
                                          q.device)
-    if ws_bytes > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    if ws_bytes > 0 and workspace is None:
+        workspace = _cached_workspace(q.device, _stream(q), ws_bytes)
+    if ws_bytes > 0 and workspace.numel() * workspace.element_size() < ws_bytes:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, "
+                         f"the call needs {ws_bytes}")
     ws_ptr = workspace.data_ptr() if (workspace is not None and ws_bytes > 0) else None
     with torch.cuda.device(q.device):
         rc = _lib.load().aegkv_paged_decode_attention(

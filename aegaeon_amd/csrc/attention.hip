@@ -12,8 +12,14 @@
 // dealt to the XCDs round-robin).  Each workgroup computes the prefix sums of
 // the batch itself (into LDS) and walks its range; a range may cut sequences,
 // whose pieces write fp32 partials (unnormalised O, running max in log2
-// units, sum) that a second kernel merges with log-sum-exp weights.  A
-// sequence held by one workgroup is normalised and written directly.
+// units, sum).  A workgroup's range can end at most one cut sequence (a cut
+// sequence ending inside a range began before it, i.e. at the range's start),
+// so each workgroup leaves a 16-byte descriptor of that sequence (or none),
+// and a second kernel of one workgroup per descriptor merges its pieces with
+// log-sum-exp weights.  (Merging in the main kernel by the last piece to
+// arrive needs device-scope release fences, which write back the XCD's L2 and
+// measured 2x slower end to end.)  A sequence held by one workgroup is normalised
+// and written directly.
 //
 // Inside a workgroup, wave w handles kv head grp * 4 + w, and all
 // G = Hq / Hkv query heads of that kv head are processed together, so each K/V
@@ -55,6 +61,7 @@ constexpr int kBlockSize = 16;
 constexpr int kHeadsPerGroup = 4;   // waves (kv heads) per workgroup
 constexpr int kMaxBatch = 2048;     // sequences per launch (LDS prefix sums); larger
                                     // batches are launched in chunks
+constexpr int kMaxWorkgroups = 8192;  // bound of n_workgroups
 constexpr int kScanPerThread = kMaxBatch / (64 * kHeadsPerGroup);
 // Cost of starting a sequence piece (block ids and q loaded, pipeline
 // primed) in units of one block: the partition balances blocks plus this
@@ -73,7 +80,6 @@ __device__ __forceinline__ int cost_units(int len) {
 template <int D>
 constexpr int pipeline_depth() { return D >= 256 ? 2 : 3; }
 constexpr float kRescaleSlack = 8.f;  // log2 headroom of the lazy softmax rescale
-constexpr int kCombineUnroll = 4;     // pieces per group loaded together by the combine
 
 template <int DT>
 struct Elem;
@@ -129,6 +135,7 @@ struct AttnArgs {
   int32_t batch;
   int32_t n_q_heads;
   int32_t n_kv_heads;
+  int32_t head_dim;
   int32_t group;     // n_q_heads / n_kv_heads
   int32_t hpg;       // query heads per workgroup: kHeadsPerGroup * group
   int32_t n_groups;  // ceil(n_kv_heads / kHeadsPerGroup)
@@ -137,26 +144,27 @@ struct AttnArgs {
   int32_t max_seq_len;  // host bound; longer device lengths are clamped to it
   uint16_t* out;
   int64_t out_bstride;  // elements
-  int32_t* cum;         // [batch + 1] block prefix sums, written by workgroup 0
+  int4* desc;           // [n_wg] cut sequence ending in each workgroup: (b, grp, w0, npieces)
   float* part_o;        // [slots][hpg][D]
   float2* part_ml;      // [slots][hpg] (running max in log2 units, sum)
 };
 
-// Workspace layout of one launch: the prefix sums, then the partials of
-// n_wg + n_groups * batch slots (a workgroup writes at most one slot per
-// sequence piece it holds; slot = workgroup + grp * batch + b is unique).
+// Workspace layout of one launch: the workgroups' descriptors, then the
+// partials of n_wg + n_groups * batch slots (a workgroup writes at most one
+// slot per sequence piece it holds; slot = workgroup + grp * batch + b is
+// unique).  Every byte the combine reads is written by the same launch.
 struct WorkspaceLayout {
-  int64_t cum_bytes, ml_bytes, o_bytes, total;
+  int64_t desc_bytes, ml_bytes, o_bytes, total;
 };
 inline WorkspaceLayout workspace_layout(int64_t batch, int64_t hpg, int64_t head_dim,
                                         int64_t n_wg, int64_t n_groups) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   const int64_t slots = n_wg + n_groups * batch;
   WorkspaceLayout w;
-  w.cum_bytes = up((batch + 1) * 4);
+  w.desc_bytes = up(n_wg * 16);
   w.ml_bytes = up(slots * hpg * 8);
   w.o_bytes = up(slots * hpg * head_dim * 4);
-  w.total = w.cum_bytes + w.ml_bytes + w.o_bytes;
+  w.total = w.desc_bytes + w.ml_bytes + w.o_bytes;
   return w;
 }
 
@@ -401,6 +409,12 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int b, int h, 
   }
 }
 
+// Workgroup that holds position P of the flattened range (the largest w with
+// floor(w * total / n_act) <= P; n_act <= total, so every range is non-empty).
+__device__ __forceinline__ int64_t owner_of(int64_t P, int64_t total, int64_t n_act) {
+  return ((P + 1) * n_act - 1) / total;
+}
+
 template <int DT, int D, int NBUF>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, D >= 256 ? 1 : 2) void
 paged_decode_attention_kernel(AttnArgs a) {
@@ -447,15 +461,24 @@ paged_decode_attention_kernel(AttnArgs a) {
     if (tid == 64 * kHeadsPerGroup - 1) s_cum[a.batch] = base + x;
     __syncthreads();
   }
-  if (blockIdx.x == 0)
-    for (int i = tid; i <= a.batch; i += 64 * kHeadsPerGroup) a.cum[i] = s_cum[i];
+  // Empty sequences have no positions: workgroup b % n_wg writes their zeros.
+  for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
+    if (s_cum[b + 1] != s_cum[b]) continue;  // uniform over the workgroup
+    uint16_t* op = a.out + (int64_t)b * a.out_bstride;
+    for (int e = tid * 8; e < a.n_q_heads * a.head_dim; e += 8 * 64 * kHeadsPerGroup)
+      *reinterpret_cast<u32x4*>(op + e) = u32x4{0u, 0u, 0u, 0u};
+  }
 
   const int64_t W = s_cum[a.batch];
   const int64_t total = W * a.n_groups;
   // With fewer positions than workgroups only the first `total` take part, so
   // that every range is non-empty.
   const int64_t n_act = min((int64_t)a.n_wg, total);
-  if ((int64_t)blockIdx.x >= n_act) return;
+  if ((int64_t)blockIdx.x >= n_act) {
+    if (tid == 0) a.desc[blockIdx.x] = make_int4(-1, 0, 0, 0);
+    return;
+  }
+  bool first_piece = true;  // the range's first piece is the only one that can end a cut sequence
   int64_t P = (int64_t)blockIdx.x * total / n_act;
   const int64_t p_end = (int64_t)(blockIdx.x + 1) * total / n_act;
   // Every value below is uniform over the workgroup.  A sequence occupies
@@ -478,99 +501,120 @@ paged_decode_attention_kernel(AttnArgs a) {
     const int nblk = s_cum[b + 1] - first;
     const int j0 = p - first;
     const int j1 = (int)min((int64_t)nblk, (int64_t)j0 + (p_end - P));
+    // pieces of (grp, b): the owners of its block positions
+    const int64_t pbase = (int64_t)grp * W;
+    const int64_t w0 = owner_of(pbase + first, total, n_act);
+    const int64_t w1 = owner_of(pbase + s_cum[b + 1] - 1, total, n_act);
     const int h = grp * kHeadsPerGroup + wave;
+    if (first_piece) {
+      first_piece = false;
+      if (tid == 0)
+        a.desc[blockIdx.x] = (w0 != w1 && j1 == nblk) ? make_int4(b, grp, (int)w0, (int)(w1 - w0 + 1))
+                                                      : make_int4(-1, 0, 0, 0);
+    }
     if (h < a.n_kv_heads)
-      attend_segment<DT, D, NBUF>(a, b, h, j0, j1, s_len[b], j0 == 0 && j1 == nblk,
+      attend_segment<DT, D, NBUF>(a, b, h, j0, j1, s_len[b], w0 == w1,
                                   (int64_t)blockIdx.x + (int64_t)grp * a.batch + b,
                                   wave * a.group);
     P += j1 - j0;
   }
+  if (first_piece && tid == 0) a.desc[blockIdx.x] = make_int4(-1, 0, 0, 0);
 }
 
-// Workgroup that holds position P of the flattened range (the largest w with
-// floor(w * total / n_act) <= P; n_act <= total, so every range is non-empty).
-__device__ __forceinline__ int64_t owner_of(int64_t P, int64_t total, int64_t n_act) {
-  return ((P + 1) * n_act - 1) / total;
-}
-
-// Finish one (sequence, query head): zeros for an empty sequence, nothing
-// when one workgroup held the whole sequence (it wrote the output), otherwise
-// merge the pieces' partials:
+// Merge the pieces of the cut sequence whose last block workgroup
+// blockIdx.x of the main kernel held (none: nothing to do), for kv head
+// grp * 4 + blockIdx.y:
 //   out = sum_s w_s o_s / sum_s w_s l_s,  w_s = 2^(m_s - max m).
-// 256 threads = NG piece groups x (D/4) lanes of 4 dims.  Each group loads up
-// to kCombineUnroll of its pieces at once (independent loads, one memory
-// latency per pass), merges them online, and the groups merge in LDS.
-template <int DT, int D>
-__global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
+// The kv head's G query heads x D/4 float4 columns are "items", spread densely
+// over the 64 lanes of a wave (KI = ceil(G * D/4 / 64) per lane, a template
+// parameter so that registers follow the group size); wave w merges pieces
+// w, w + 4, ... online (two loaded at a time, so four waves cover eight pieces
+// per memory round trip), and the four waves' states merge in LDS.
+template <int DT, int D, int KI>
+__global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(AttnArgs a) {
   using E = Elem<DT>;
-  constexpr int LPS = D / 4;      // lanes per piece row
-  constexpr int NG = 256 / LPS;   // piece groups
-  constexpr int U = kCombineUnroll;
-  __shared__ float s_m[NG], s_l[NG];
-  __shared__ f32x4 s_o[NG][LPS];
-  const int hq = blockIdx.x, b = blockIdx.y;
-  const int grp_ln = threadIdx.x % LPS;
-  const int c0 = a.cum[b], c1 = a.cum[b + 1];
-  uint16_t* op = a.out + (int64_t)b * a.out_bstride + (int64_t)hq * D + 4 * grp_ln;
-  if (c1 == c0) {  // empty sequence (uniform over the workgroup)
-    if (threadIdx.x < LPS) *reinterpret_cast<u32x2*>(op) = u32x2{0u, 0u};
-    return;
+  constexpr int D4 = D / 4;                // float4 per query head
+  constexpr int U = KI >= 8 ? 1 : 2;       // pieces loaded together per wave
+  __shared__ float s_m[kHeadsPerGroup - 1][KI][64];
+  __shared__ float s_l[kHeadsPerGroup - 1][KI][64];
+  __shared__ f32x4 s_o[kHeadsPerGroup - 1][KI][64];
+  const int4 d = a.desc[blockIdx.x];
+  if (d.x < 0) return;  // uniform over the workgroup
+  const int b = d.x, grp = d.y, npieces = d.w;
+  const int h = grp * kHeadsPerGroup + blockIdx.y;
+  if (h >= a.n_kv_heads) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int items = a.group * D4;
+  const int64_t slot0 = (int64_t)d.z + (int64_t)grp * a.batch + b;
+  const int hl0 = blockIdx.y * a.group;  // first query head of h within a slot
+  float m[KI], l[KI];
+  f32x4 o[KI];
+#pragma unroll
+  for (int k = 0; k < KI; ++k) {
+    m[k] = -INFINITY;
+    l[k] = 0.f;
+    o[k] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // the pieces are the owners of the sequence's block positions
-  // [c0 + kSegmentCost, c1) of group grp
-  const int h = hq / a.group, grp = h / kHeadsPerGroup;
-  const int64_t total = (int64_t)a.cum[a.batch] * a.n_groups;
-  const int64_t n_act = min((int64_t)a.n_wg, total);
-  const int64_t P0 = (int64_t)grp * a.cum[a.batch] + c0 + kSegmentCost;
-  const int64_t w0 = owner_of(P0, total, n_act);
-  const int64_t w1 = owner_of((int64_t)grp * a.cum[a.batch] + c1 - 1, total, n_act);
-  if (w0 == w1) return;
-  const int npieces = (int)(w1 - w0 + 1);
-  const int64_t slot0 = w0 + (int64_t)grp * a.batch + b;
-  const int hl = hq - grp * kHeadsPerGroup * a.group;
-  const int pg = threadIdx.x / LPS, ln = grp_ln;
-  float m = -INFINITY, l = 0.f;
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = pg; s0 < npieces; s0 += NG * U) {
-    float2 ml[U];
-    f32x4 po[U];
+  for (int s0 = wave; s0 < npieces; s0 += kHeadsPerGroup * U) {
+    float2 ml[U][KI];
+    f32x4 po[U][KI];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int s = s0 + u * NG;
-      ml[u] = make_float2(-INFINITY, 0.f);
-      po[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (s < npieces) {
-        const int64_t pidx = (slot0 + s) * a.hpg + hl;
-        ml[u] = a.part_ml[pidx];
-        po[u] = *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + 4 * ln);
+      const int sp = s0 + u * kHeadsPerGroup;
+#pragma unroll
+      for (int k = 0; k < KI; ++k) {
+        const int it = lane + 64 * k;
+        ml[u][k] = make_float2(-INFINITY, 0.f);
+        if (sp < npieces && it < items) {
+          const int64_t pidx = (slot0 + sp) * a.hpg + hl0 + it / D4;
+          ml[u][k] = a.part_ml[pidx];
+          po[u][k] = *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + 4 * (it % D4));
+        }
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (ml[u].x == -INFINITY) continue;  // absent, or a piece with no readable block
-      const float mn = fmaxf(m, ml[u].x);
-      const float wa = __builtin_amdgcn_exp2f(m - mn), wb = __builtin_amdgcn_exp2f(ml[u].x - mn);
-      o = o * wa + po[u] * wb;
-      l = l * wa + ml[u].y * wb;
-      m = mn;
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int k = 0; k < KI; ++k) {
+        if (ml[u][k].x == -INFINITY) continue;  // absent, or a piece with no readable block
+        const float mn = fmaxf(m[k], ml[u][k].x);
+        const float wa = __builtin_amdgcn_exp2f(m[k] - mn);
+        const float wb = __builtin_amdgcn_exp2f(ml[u][k].x - mn);
+        o[k] = o[k] * wa + po[u][k] * wb;
+        l[k] = l[k] * wa + ml[u][k].y * wb;
+        m[k] = mn;
+      }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+      s_m[wave - 1][k][lane] = m[k];
+      s_l[wave - 1][k][lane] = l[k];
+      s_o[wave - 1][k][lane] = o[k];
     }
   }
-  if (ln == 0) { s_m[pg] = m; s_l[pg] = l; }
-  s_o[pg][ln] = o;
   __syncthreads();
-  if (pg == 0) {
-    float mx = -INFINITY;
+  if (wave > 0) return;
 #pragma unroll
-    for (int k = 0; k < NG; ++k) mx = fmaxf(mx, s_m[k]);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float lt = 0.f;
+  for (int k = 0; k < KI; ++k) {
+    const int it = lane + 64 * k;
+    if (it >= items) continue;
+    float mx = m[k];
 #pragma unroll
-    for (int k = 0; k < NG; ++k) {
-      const float w = s_m[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[k] - mx);
-      acc += s_o[k][ln] * w;
-      lt += s_l[k] * w;
+    for (int w = 0; w < kHeadsPerGroup - 1; ++w) mx = fmaxf(mx, s_m[w][k][lane]);
+    const float w0 = m[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[k] - mx);
+    f32x4 acc = o[k] * w0;
+    float lt = l[k] * w0;
+#pragma unroll
+    for (int w = 0; w < kHeadsPerGroup - 1; ++w) {
+      const float mw = s_m[w][k][lane];
+      const float ww = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
+      acc += s_o[w][k][lane] * ww;
+      lt += s_l[w][k][lane] * ww;
     }
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t* op = a.out + (int64_t)b * a.out_bstride +
+                   (int64_t)(h * a.group + it / D4) * D + 4 * (it % D4);
     *reinterpret_cast<u32x2*>(op) =
         u32x2{E::bits(acc[0] * inv) | (E::bits(acc[1] * inv) << 16),
               E::bits(acc[2] * inv) | (E::bits(acc[3] * inv) << 16)};
@@ -590,7 +634,15 @@ int workgroups_for(int32_t requested, int* n_wg) {
   DeviceState* ds = nullptr;
   int rc = current_device_state(&ds);
   if (rc) return rc;
-  *n_wg = std::max(1, ds->num_cu);
+  *n_wg = std::min(std::max(1, ds->num_cu), kMaxWorkgroups);
+  return AEGKV_OK;
+}
+
+template <int DT, int D, int KI>
+int launch_combine(const AttnArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI>), dim3(a.n_wg, kHeadsPerGroup),
+                     dim3(64 * kHeadsPerGroup), 0, stream, a);
+  AEGKV_HIP_TRY(hipGetLastError());
   return AEGKV_OK;
 }
 
@@ -599,10 +651,12 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>()>), dim3(a.n_wg),
                      dim3(64 * kHeadsPerGroup), lds_bytes(a.batch), stream, a);
   AEGKV_HIP_TRY(hipGetLastError());
-  hipLaunchKernelGGL((attention_combine_kernel<DT, D>), dim3(a.n_q_heads, a.batch), dim3(256),
-                     0, stream, a);
-  AEGKV_HIP_TRY(hipGetLastError());
-  return AEGKV_OK;
+  const int items = a.group * (D / 4);  // <= 16 * D / 4
+  if (items <= 64) return launch_combine<DT, D, 1>(a, stream);
+  if (items <= 128) return launch_combine<DT, D, 2>(a, stream);
+  if (items <= 256) return launch_combine<DT, D, 4>(a, stream);
+  if (items <= 512) return launch_combine<DT, D, 8>(a, stream);
+  return launch_combine<DT, D, 16>(a, stream);
 }
 
 }  // namespace
@@ -619,6 +673,7 @@ int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_h
   if (batch < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads ||
       n_workgroups < 0 || max_seq_len < 0)
     return AEGKV_ERR_INVALID_ARG;
+  if (n_workgroups > kMaxWorkgroups) return AEGKV_ERR_UNSUPPORTED;
   if ((head_dim != 64 && head_dim != 128 && head_dim != 256) ||
       (dtype != AEGKV_DTYPE_BF16 && dtype != AEGKV_DTYPE_FP16) || n_q_heads / n_kv_heads > 16)
     return AEGKV_ERR_UNSUPPORTED;
@@ -657,7 +712,7 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
       ((q_batch_stride * 2) & 15) || ((out_batch_stride * 2) & 15) ||
       ((cache_block_stride * 2) & 15))
     return AEGKV_ERR_MISALIGNED;
-  if (n_q_heads > 65535) return AEGKV_ERR_UNSUPPORTED;
+  if (n_q_heads > 65535 || n_workgroups > kMaxWorkgroups) return AEGKV_ERR_UNSUPPORTED;
   const int64_t nblk_max = ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize;
   if (nblk_max > max_blocks) return AEGKV_ERR_INVALID_ARG;
   const int32_t chunk = std::min(batch, kMaxBatch);
@@ -680,6 +735,7 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
   a.max_blocks = max_blocks;
   a.n_q_heads = n_q_heads;
   a.n_kv_heads = n_kv_heads;
+  a.head_dim = head_dim;
   a.group = group;
   a.hpg = kHeadsPerGroup * group;
   a.n_groups = n_groups;
@@ -688,9 +744,9 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
   a.max_seq_len = max_seq_len;
   a.q_bstride = q_batch_stride;
   a.out_bstride = out_batch_stride;
-  a.cum = reinterpret_cast<int32_t*>(ws);
-  a.part_ml = reinterpret_cast<float2*>(ws + lay.cum_bytes);
-  a.part_o = reinterpret_cast<float*>(ws + lay.cum_bytes + lay.ml_bytes);
+  a.desc = reinterpret_cast<int4*>(ws);
+  a.part_ml = reinterpret_cast<float2*>(ws + lay.desc_bytes);
+  a.part_o = reinterpret_cast<float*>(ws + lay.desc_bytes + lay.ml_bytes);
   hipStream_t st = (hipStream_t)stream;
   const bool bf = dtype == AEGKV_DTYPE_BF16;
   // Batches above kMaxBatch run as consecutive launches of kMaxBatch sequences

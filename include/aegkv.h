@@ -168,13 +168,14 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
  *   max_seq_len: host upper bound of seq_lens; device lengths above it are
  *     clamped to it, so a wrong bound never reads or writes out of bounds.
  *   n_workgroups: workgroups that share the batch's KV blocks in equal
- *     contiguous ranges (0 = the device's resident capacity, the fast choice;
- *     any positive count gives the same result).
+ *     contiguous ranges (0 = one per CU, the fast choice; 1..8192 give the
+ *     same result).
  *   workspace: DEVICE scratch of
  *     aegkv_paged_decode_attention_workspace_size(...) bytes (same batch, heads,
  *     head_dim, max_seq_len, dtype, n_workgroups and device); it holds the
- *     batch's block prefix sums and the partials of sequences that several
- *     workgroups share.  Its contents need no initialisation.
+ *     partials of sequences that several workgroups share; its contents need
+ *     no initialisation.  Calls that may run concurrently (other streams) must
+ *     not share a workspace.
  * Supported: block_size 16, head_dim 64/128/256, n_q_heads/n_kv_heads <= 16
  * (AEGKV_ERR_UNSUPPORTED otherwise).  Batches above 2048 sequences run as
  * consecutive launches of 2048.  seq_lens[b] == 0 yields zeros.  A block id

@@ -122,16 +122,18 @@ def test_attention_argument_checks_and_workspace_size(lib):
     assert ws(4, 30, 4, 128, 4096, 0, 8) == INVALID
     assert ws(4, 28, 4, 128, 4096, 9, 8) == UNSUP
     assert ws(4, 28, 4, 128, 4096, 0, -1) == INVALID
-    # prefix sums (batch + 1 int32, 256-byte aligned), then (n_wg + groups*batch)
-    # slots of hpg = 4 * 7 query heads: float2 (m, l) and D floats each
+    # one 16-byte descriptor per workgroup, then (n_wg + groups*batch) slots
+    # of hpg = 4 * 7 query heads: float2 (m, l) and D floats each
+    up = lambda x: -(-x // 256) * 256  # noqa: E731
+    cnt = up(8 * 16)
     slots = 8 + 1 * 4
-    want = 256 + -(-slots * 28 * 8 // 256) * 256 + -(-slots * 28 * 128 * 4 // 256) * 256
+    want = cnt + up(slots * 28 * 8) + up(slots * 28 * 128 * 4)
     assert ws(4, 28, 4, 128, 4096, 0, 8) == want
     assert ws(4, 28, 4, 128, 4096, 0, 16) > want
     # Llama-shaped 40/40: ten groups of four kv heads, one query head each
     slots = 8 + 10 * 4
-    assert ws(4, 40, 40, 128, 4096, 1, 8) == (
-        256 + -(-slots * 4 * 8 // 256) * 256 + -(-slots * 4 * 128 * 4 // 256) * 256)
+    assert ws(4, 40, 40, 128, 4096, 1, 8) == cnt + up(slots * 4 * 8) + up(slots * 4 * 128 * 4)
+    assert ws(4, 28, 4, 128, 4096, 0, 8193) == UNSUP
     # batches above 2048 are launched in chunks of 2048 sharing one workspace
     assert ws(5000, 28, 4, 128, 4096, 0, 8) == ws(2048, 28, 4, 128, 4096, 0, 8)
 
@@ -148,6 +150,7 @@ def test_attention_argument_checks_and_workspace_size(lib):
     assert attn(Hq=34, Hkv=2) == UNSUP  # group of 17 > 16
     assert attn(max_len=100) == INVALID  # needs 7 blocks, table has 4
     assert attn(nwg=-1) == INVALID
+    assert attn(nwg=8193) == UNSUP
     need = ws(2, 28, 4, 128, 4096, 0, 1)
     assert need > 0
     assert attn(max_len=4096, max_blocks=256, nwg=1) == WS

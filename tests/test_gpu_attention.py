@@ -210,3 +210,25 @@ def test_qwen_full_batch_layer(device):
     ref = ko.paged_decode_attention(ko.bits_to_float(q, "bf16"), ko.bits_to_float(k_used, "bf16"),
                                     ko.bits_to_float(v_used, "bf16"), compact, lens, scale)
     _check(to_bits(out), ref, "bf16")
+
+
+def test_workspace_reused_across_calls(device):
+    """One workspace serves consecutive calls of different batches: nothing a
+    call leaves in it may leak into the next (stale partials, descriptors)."""
+    ws = A.attention_workspace(8, 28, 4, 128, 2000, torch.bfloat16, n_workgroups=5,
+                               device=device)
+    ws.fill_(0x7F)  # stale bytes: the result must not depend on the contents
+    for seed, lens in ((21, [900, 3, 1500, 40, 0, 17, 700, 2000]),
+                       (22, [1, 2, 3, 4]),
+                       (21, [900, 3, 1500, 40, 0, 17, 700, 2000])):
+        rng = np.random.default_rng(seed)
+        lens, tables, padded, q, kc, vc = _setup(rng, lens, 28, 4, 128, "bf16", pad_to=125)
+        scale = 1.0 / math.sqrt(128)
+        out = A.paged_decode_attention(
+            to_device_bits(q, "bf16", device), to_device_bits(kc, "bf16", device),
+            to_device_bits(vc, "bf16", device), torch.from_numpy(padded).to(device),
+            torch.from_numpy(lens.astype(np.int32)).to(device), scale, 2000, n_workgroups=5,
+            workspace=ws)
+        ref = ko.paged_decode_attention(ko.bits_to_float(q, "bf16"), ko.bits_to_float(kc, "bf16"),
+                                        ko.bits_to_float(vc, "bf16"), padded, lens, scale)
+        _check(to_bits(out), ref, "bf16")
