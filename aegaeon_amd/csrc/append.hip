@@ -16,8 +16,8 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kAppendThreads = 256;
-constexpr int kAppendItems = 4;  // 16-byte chunks per lane, loads issued before stores
+constexpr int kAppendThreads = 64;
+constexpr int kAppendItems = 1;  // 16-byte chunks per lane
 
 // Chunk c of the flattened (layer, kv, token, row-chunk) space.
 struct AppendArgs {
@@ -35,10 +35,16 @@ struct AppendArgs {
   uint32_t total_chunks;   // n_layers * 2 * n_tokens * row_chunks
 };
 
-// The source row of a chunk does not depend on its slot, so the K/V loads and
-// the slot loads of all kAppendItems chunks are issued together; only the
-// stores wait for the slots.  That keeps the dependent-latency chain at one
-// HBM round trip plus the store.
+// The source row of a chunk does not depend on its slot, so the K/V load and
+// the slot load are issued together; only the store waits for the slot.  That
+// keeps the dependent-latency chain at one HBM round trip plus the store.
+// One chunk per lane in 64-lane workgroups (a wave per 1 KiB row at the
+// Qwen2.5-7B shape) measured fastest on MI355X: the step is a single burst of
+// loads and stores, and spreading it over the most workgroups (3584 for the
+// 256-token x 28-layer step, 128 for one layer) shortens the burst; 2-8
+// chunks per lane and 256-512-lane workgroups were 2-65% slower.  The K/V
+// rows are read once and the cache rows are not read again before the
+// attention of the step streams them, so both sides are non-temporal.
 __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(AppendArgs a) {
   const uint32_t nthreads = gridDim.x * kAppendThreads;
   const uint32_t gid = blockIdx.x * kAppendThreads + threadIdx.x;
@@ -68,7 +74,7 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(AppendArgs a)
       const uint32_t layer = lk[k] >> 1, kv = lk[k] & 1;
       uint8_t* dst = (kv ? a.vc : a.kc) + layer * a.layer_b + blk * a.blk_b +
                      off * (int64_t)a.row_chunks * 16;
-      reinterpret_cast<u32x4*>(dst)[chunk[k]] = r[k];
+      __builtin_nontemporal_store(r[k], reinterpret_cast<u32x4*>(dst) + chunk[k]);
     }
   }
 }
