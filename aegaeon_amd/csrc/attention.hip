@@ -300,15 +300,6 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int b, int h, 
   const bool head_ok = j < a.group;
   const int hq = h * a.group + j;
 
-  u32x4 qv[KS];
-  {
-    const uint16_t* qp = a.q + (int64_t)b * a.q_bstride + (int64_t)(head_ok ? hq : 0) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u32x4 v = *reinterpret_cast<const u32x4*>(qp + 32 * ks + 8 * g);
-      qv[ks] = head_ok ? v : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
 
   f32x4 acc[DPL];
 #pragma unroll
@@ -320,14 +311,27 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int b, int h, 
   const uint16_t* vh = a.vc + (int64_t)h * D + (int64_t)(4 * g) * row + DPL * j;
   const int32_t* bt = a.block_tables + (int64_t)b * a.max_blocks;
 
+  // Block ids are loaded one 64-block chunk ahead, unconditionally (clamped
+  // index, masked at use) so that no load sits under a branch; the first
+  // chunk's are loaded before q: the waits are in issue order, so the K/V
+  // loads that need the ids can start while q is in flight.
+  int id_next = bt[min(j0 + lane, j1 - 1)];
+  // Lanes past the group load the group's first head: every head column of
+  // the products and of the softmax is independent and only real heads are
+  // written, so no select has to wait for q here.
+  u32x4 qv[KS];
+  {
+    const uint16_t* qp = a.q + (int64_t)b * a.q_bstride + (int64_t)(head_ok ? hq : h * a.group) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qv[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks + 8 * g);
+  }
+
   for (int c0 = j0; c0 < j1; c0 += 64) {
     const int nb = min(64, j1 - c0);
     // block ids of this chunk, one per lane; ids outside the pool become -1
-    int my_id = -1;
-    if (lane < nb) {
-      const int id = bt[c0 + lane];
-      my_id = (id >= 0 && id < a.n_blocks) ? id : -1;
-    }
+    const int id = id_next;
+    const int my_id = (lane < nb && id >= 0 && id < a.n_blocks) ? id : -1;
+    id_next = bt[min(c0 + 64 + lane, j1 - 1)];
     // Rolling register pipeline of NBUF blocks: buffer k holds block i = it + k;
     // as soon as block i is computed, its buffer is refilled with block
     // i + NBUF, so NBUF - 1 blocks stay in flight while a block is computed and
@@ -433,10 +437,12 @@ paged_decode_attention_kernel(AttnArgs a) {
     const int b0 = tid * per;
     int lens[kScanPerThread];
     int cnt = 0;
+    // all loads issued before any is used (clamped index, masked after)
+#pragma unroll
+    for (int k = 0; k < kScanPerThread; ++k) lens[k] = a.seq_lens[min(b0 + k, a.batch - 1)];
 #pragma unroll
     for (int k = 0; k < kScanPerThread; ++k) {
-      lens[k] = 0;
-      if (k < per && b0 + k < a.batch) lens[k] = min(max(a.seq_lens[b0 + k], 0), a.max_seq_len);
+      lens[k] = (k < per && b0 + k < a.batch) ? min(max(lens[k], 0), a.max_seq_len) : 0;
       cnt += cost_units(lens[k]);
     }
     int x = cnt;
