@@ -44,6 +44,9 @@ SIGNATURES: Dict[str, tuple] = {
                                     c_int32, c_int32, c_void_p]),
     "aegkv_paged_decode_attention_workspace_size": (c_int64, [c_int32, c_int32, c_int32, c_int32,
                                                               c_int32, c_int32, c_int32]),
+    "aegkv_prepare_inputs": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
+                                     c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
+                                     c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "aegkv_paged_decode_attention": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                              c_void_p, c_int64, c_int64, c_void_p, c_int32,
                                              c_void_p, c_int32, c_int32, c_int32, c_int32,

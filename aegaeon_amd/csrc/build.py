@@ -19,7 +19,7 @@ ROOT = PKG.parent
 BUILD_DIR = ROOT / "_build"
 LIB_PATH = PKG / "libaegkv.so"
 
-SOURCES = ["runtime.hip", "blocks.hip", "append.hip", "attention.hip"]
+SOURCES = ["runtime.hip", "blocks.hip", "append.hip", "attention.hip", "inputs.hip"]
 ARCH = "gfx950"
 
 # Packed FP32 instructions are disabled for every HIP translation unit.

@@ -1,0 +1,112 @@
+"""Per-step model inputs built on the GPU, with the reference's outputs.
+
+:func:`prepare_model_inputs` takes what ``Worker._prepare_model_inputs``
+(aegaeon/aegaeon/worker.py:554-713) takes — the batch's ``RequestMeta`` tuples
+``(request_id, tokens, seq_len, context_len)`` (aegaeon/aegaeon/request.py:
+96-102), sorted prefill -> decode, and their block tables — and returns the
+same ``(input_tokens, input_positions, metadata)``, where ``metadata`` holds the
+keyword arguments the reference passes to the attention backend's
+``make_metadata`` (worker.py:694-711).  The per-token slot-mapping loop
+(worker.py:628-633), the 0-padded table build (utils.py:241-257) and the eight
+host-to-device tensors become one upload and one gfx950 kernel
+(``aegkv_prepare_inputs``).
+"""
+from __future__ import annotations
+
+import itertools
+from typing import Dict, List, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+
+BLOCK_SIZE = 16  # aegaeon/aegaeon/config.py:13
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data if a.size else None
+
+
+def prepare_model_inputs(requests: Sequence[Tuple], block_tables: Sequence[Sequence[int]],
+                         device, block_size: int = BLOCK_SIZE
+                         ) -> Tuple[torch.Tensor, torch.Tensor, Dict]:
+    """GPU form of ``Worker._prepare_model_inputs``.
+
+    Returns ``(input_tokens int64 [T], input_positions int64 [T], metadata)``
+    with ``metadata`` = ``num_prefills, slot_mapping (int64 [T]),
+    num_prefill_tokens, num_decode_tokens, seq_lens (list), seq_lens_tensor
+    (int32), max_query_len, max_prefill_seq_len, max_decode_seq_len,
+    query_start_loc (int32 [B+1]), seq_start_loc (int32 [B+1]),
+    context_lens_tensor (int32), block_tables (int32 [B, max table len]),
+    use_cuda_graph=False``.  Raises ``AegkvError`` for a table that does not
+    cover its sequence, like the reference's index error.
+    """
+    if len(requests) == 0:
+        raise ValueError("empty batch")  # the reference asserts (worker.py:594)
+    if len(block_tables) != len(requests):
+        raise ValueError("one block table per request")
+    device = torch.device(device)
+    B = len(requests)
+    # one C-speed pass over each list (the lists are the block manager's)
+    seq = np.fromiter((r[2] for r in requests), dtype=np.int32, count=B)
+    ctx = np.fromiter((r[3] for r in requests), dtype=np.int32, count=B)
+    qlen = seq.astype(np.int64) - ctx
+    is_prompt = ctx == 0
+    ntok = np.fromiter((len(r[1]) for r in requests), dtype=np.int64, count=B)
+    if not np.array_equal(ntok, qlen):
+        raise ValueError("a request's tokens must be its seq_len - context_len new tokens")
+    lens = np.fromiter(map(len, block_tables), dtype=np.int64, count=B)
+    offsets = np.zeros(B + 1, dtype=np.int64)
+    np.cumsum(lens, out=offsets[1:])
+    ids = np.fromiter(itertools.chain.from_iterable(block_tables), dtype=np.int32,
+                      count=int(offsets[-1]))
+    tokens = np.fromiter(itertools.chain.from_iterable(r[1] for r in requests), dtype=np.int64,
+                         count=int(qlen.sum()))
+    # decode rows keep their table, prefill rows are empty (worker.py:600-605)
+    pad_width = int(lens[~is_prompt].max()) if (~is_prompt).any() else 0
+    T = int(qlen.sum())
+
+    i32 = dict(dtype=torch.int32, device=device)
+    i64 = dict(dtype=torch.int64, device=device)
+    bt_out = torch.empty((B, pad_width), **i32)
+    slots = torch.empty(T, **i64)
+    positions = torch.empty(T, **i64)
+    toks = torch.empty(T, **i64)
+    seq_t = torch.empty(B, **i32)
+    ctx_t = torch.empty(B, **i32)
+    qsl = torch.empty(B + 1, **i32)
+    ssl = torch.empty(B + 1, **i32)
+    with torch.cuda.device(device):
+        rc = _lib.load().aegkv_prepare_inputs(
+            _ptr(ids), offsets.ctypes.data, seq.ctypes.data, ctx.ctypes.data, _ptr(tokens), B,
+            block_size, pad_width, bt_out.data_ptr() if pad_width else None,
+            slots.data_ptr() if T else None, positions.data_ptr() if T else None,
+            toks.data_ptr() if T else None, seq_t.data_ptr(), ctx_t.data_ptr(), qsl.data_ptr(),
+            ssl.data_ptr(), T, torch.cuda.current_stream(device).cuda_stream)
+    _lib.check(rc, "prepare_model_inputs")
+    prefill_lens = seq[is_prompt]
+    decode_lens = seq[~is_prompt]
+    metadata = dict(
+        num_prefills=int(is_prompt.sum()),
+        slot_mapping=slots,
+        num_prefill_tokens=int(qlen[is_prompt].sum()),
+        num_decode_tokens=int(qlen[~is_prompt].sum()),
+        seq_lens=[int(x) for x in seq],
+        seq_lens_tensor=seq_t,
+        max_query_len=int(qlen.max()),
+        max_prefill_seq_len=int(prefill_lens.max()) if prefill_lens.size else 0,
+        max_decode_seq_len=int(decode_lens.max()) if decode_lens.size else 0,
+        query_start_loc=qsl,
+        seq_start_loc=ssl,
+        context_lens_tensor=ctx_t,
+        block_tables=bt_out,
+        use_cuda_graph=False,
+    )
+    return toks, positions, metadata
+
+
+def decode_requests(context_lens: Sequence[int], first_token: int = 0) -> List[Tuple]:
+    """``RequestMeta`` tuples of a decode batch: request i holds
+    ``context_lens[i]`` cached tokens and decodes one more."""
+    return [(i, [first_token + i], int(c) + 1, int(c)) for i, c in enumerate(context_lens)]

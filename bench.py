@@ -360,6 +360,51 @@ def bench_gather(args, timer):
     return {"bytes": nbytes, "ms": region_ms}
 
 
+# ------------------------------------------------------------- input preparation
+def bench_prepare(args, timer):
+    """Per-step metadata (slot mapping, padded tables, lengths, start offsets)
+    for the Qwen2.5-7B decode batch (256 requests) and a prefill batch (8
+    prompts of 2048 tokens): the library's one upload + one kernel against the
+    reference's host loops (the oracle's restatement of worker.py:596-676)
+    followed by the reference's eight host-to-device tensors.  Wall time per
+    step, synchronised, host work included."""
+    import torch
+    from aegaeon_amd import inputs as I
+    from aegaeon_amd.workloads import qwen_append_batch
+    from oracle import kv_oracle as ko
+    dev = torch.device("cuda", 0)
+    wb = qwen_append_batch(args.seed)
+    rng = np.random.default_rng(args.seed)
+    perm = iter(rng.permutation(8 * 128).tolist())
+    pre_tables = [[next(perm) for _ in range(128)] for _ in range(8)]
+    pre_reqs = [(i, rng.integers(0, 32000, 2048).tolist(), 2048, 0) for i in range(8)]
+    cases = {"qwen_decode_256": (I.decode_requests(wb.context_lens), wb.block_tables),
+             "prefill_8x2048": (pre_reqs, pre_tables)}
+    out = {}
+
+    def reference_path(reqs, tables):
+        r = ko.prepare_model_inputs(reqs, tables)
+        for k in ("input_tokens", "input_positions", "slot_mapping", "block_tables",
+                  "seq_lens_tensor", "context_lens_tensor", "query_start_loc", "seq_start_loc"):
+            torch.from_numpy(np.ascontiguousarray(r[k])).to(dev)
+
+    for name, (reqs, tables) in cases.items():
+        times = {}
+        for label, fn in (("device", lambda: I.prepare_model_inputs(reqs, tables, dev)),
+                          ("reference_host", lambda: reference_path(reqs, tables))):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 0.5 or n < 5:
+                fn()
+                torch.cuda.synchronize()
+                n += 1
+            times[label] = (time.perf_counter() - t0) / n * 1e6
+        out[name] = times
+    return out
+
+
 # ------------------------------------------------------------------ copy calibration
 CALIB_BLOCKS, CALIB_BLOCK_BYTES = 256, 1 << 20
 
@@ -454,7 +499,7 @@ def main(argv=None):
     p.add_argument("--swap-seqs", type=int, default=32)
     p.add_argument("--pcie-blocks", type=int, default=64)
     p.add_argument("--only", default="all",
-                   help="comma list of append,attention,pack,defrag,gather,calib or 'all'")
+                   help="comma list of append,attention,pack,defrag,gather,prepare,calib or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU and "
@@ -469,13 +514,13 @@ def main(argv=None):
     torch.cuda.set_device(0)
     log(f"device: {torch.cuda.get_device_name(0)}")
     only = set(args.only.split(",")) if args.only != "all" else \
-        {"append", "attention", "pack", "defrag", "gather", "calib"}
+        {"append", "attention", "pack", "defrag", "gather", "prepare", "calib"}
     timer = Timer()
     log(f"spin calibration: {timer.cycles_per_ms:.0f} cycles/ms")
     res = {}
     for name, fn in (("append", bench_append), ("attention", bench_attention),
                      ("gather", bench_gather), ("pack", bench_pack), ("defrag", bench_defrag),
-                     ("calib", bench_calib)):
+                     ("prepare", bench_prepare), ("calib", bench_calib)):
         if name in only:
             t0 = time.perf_counter()
             res[name] = fn(args, timer)
@@ -551,6 +596,10 @@ def main(argv=None):
             "yi_append_us": round(d["yi_append_ms"] * 1e3, 2), "yi_append_GB/s": round(ag, 1),
             "yi_attention_us_per_layer": round(d["yi_attn_us_per_layer"], 2),
             "yi_attention_GB/s": round(tg, 1), "yi_attention_frac_hbm": round(tg / HBM_PEAK_GBS, 4)}
+    if "prepare" in res:
+        ops_out["prepare_inputs_us_per_step"] = {
+            k: {"device": round(v["device"], 1), "reference_host_loops": round(v["reference_host"], 1)}
+            for k, v in res["prepare"].items()}
     if "calib" in res:
         c = res["calib"]
         cg = c["bytes"] / (c["ms"] * 1e-3) / 1e9

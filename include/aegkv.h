@@ -198,6 +198,34 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
                                  int32_t n_workgroups, void* workspace,
                                  uint64_t workspace_bytes, aegkv_stream_t stream);
 
+/* ---- a4: decode/prefill input preparation --------------------------------
+ * Replaces the host loops of Worker._prepare_model_inputs
+ * (aegaeon/aegaeon/worker.py:596-676) and make_tensor_with_pad
+ * (aegaeon/aegaeon/utils.py:241-257): one upload of the HOST request lists and
+ * one kernel that writes the DEVICE tensors the attention metadata holds.
+ * Request b has block table block_ids[table_offsets[b] .. table_offsets[b+1]),
+ * total length seq_lens[b] and first new token context_lens[b]
+ * (request.py:96-102); its new tokens are tokens[q0 .. q0 + seq - ctx) with
+ * q0 the sum of the previous requests' (seq - ctx).  Outputs (DEVICE):
+ *   block_tables_out [batch][pad_width] int32: the table of a decode row
+ *     (context_lens[b] > 0), 0-padded; prefill rows all 0 (worker.py:600-605);
+ *   slot_mapping_out [n_query_tokens] int64: table[p / bs] * bs + p % bs for
+ *     p in [context_len, seq_len) (worker.py:628-633);
+ *   positions_out [n_query_tokens] int64: p;  input_tokens_out (may be NULL):
+ *     the tokens;  seq_lens_out, context_lens_out [batch] int32;
+ *   query_start_loc_out, seq_start_loc_out [batch + 1] int32 prefix sums.
+ * Host checks: context_len <= seq_len, every table covers (seq_len - 1) / bs,
+ * decode tables fit pad_width, n_query_tokens = sum(seq - ctx), ids >= 0. */
+int aegkv_prepare_inputs(const int32_t* block_ids, const int64_t* table_offsets,
+                         const int32_t* seq_lens, const int32_t* context_lens,
+                         const int64_t* tokens, int32_t batch, int32_t block_size,
+                         int32_t pad_width, int32_t* block_tables_out,
+                         int64_t* slot_mapping_out, int64_t* positions_out,
+                         int64_t* input_tokens_out, int32_t* seq_lens_out,
+                         int32_t* context_lens_out, int32_t* query_start_loc_out,
+                         int32_t* seq_start_loc_out, int64_t n_query_tokens,
+                         aegkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -85,6 +85,52 @@ def pad_block_tables(tables: Sequence[Sequence[int]], pad: int = 0) -> np.ndarra
     return out
 
 
+def prepare_model_inputs(requests, block_tables, block_size: int = BLOCK_SIZE):
+    """Restatement of ``Worker._prepare_model_inputs`` (worker.py:596-676),
+    host loops included: returns a dict of numpy arrays / ints with the
+    reference's names and dtypes (input_tokens, input_positions, slot_mapping
+    int64; block_tables, seq_lens_tensor, context_lens_tensor,
+    query_start_loc, seq_start_loc int32)."""
+    input_tokens, input_positions, slot_mapping = [], [], []
+    seq_lens, prefill_seq_lens, decode_seq_lens, context_lens, query_lens = [], [], [], [], []
+    tables = []
+    num_prefills = num_prefill_tokens = num_decode_tokens = 0
+    for (_, tokens, seq_len, context_len), _bt in zip(requests, block_tables):
+        is_prompt = context_len == 0
+        tables.append(list(_bt) if not is_prompt else [])          # worker.py:600-605
+        seq_lens.append(seq_len)
+        context_lens.append(context_len)
+        query_lens.append(seq_len - context_len)
+        input_tokens.extend(tokens)
+        input_positions.extend(range(context_len, seq_len))
+        if is_prompt:
+            num_prefills += 1
+            num_prefill_tokens += len(tokens)
+            prefill_seq_lens.append(seq_len)
+        else:
+            num_decode_tokens += seq_len - context_len
+            decode_seq_lens.append(seq_len)
+        for i in range(context_len, seq_len):                        # worker.py:628-633
+            slot_mapping.append(_bt[i // block_size] * block_size + i % block_size)
+    width = max(len(t) for t in tables)
+    padded = pad_block_tables(tables) if width else np.zeros((len(tables), 0), dtype=np.int32)
+    q = np.asarray(query_lens, dtype=np.int64)
+    sl = np.asarray(seq_lens, dtype=np.int32)
+    return dict(
+        input_tokens=np.asarray(input_tokens, dtype=np.int64),
+        input_positions=np.asarray(input_positions, dtype=np.int64),
+        slot_mapping=np.asarray(slot_mapping, dtype=np.int64),
+        num_prefills=num_prefills, num_prefill_tokens=num_prefill_tokens,
+        num_decode_tokens=num_decode_tokens, seq_lens=list(seq_lens),
+        seq_lens_tensor=sl, context_lens_tensor=np.asarray(context_lens, dtype=np.int32),
+        max_query_len=int(q.max()), max_prefill_seq_len=max(prefill_seq_lens, default=0),
+        max_decode_seq_len=max(decode_seq_lens, default=0),
+        query_start_loc=np.concatenate([[0], np.cumsum(q)]).astype(np.int32),
+        seq_start_loc=np.concatenate([[0], np.cumsum(sl)]).astype(np.int32),
+        block_tables=padded,
+    )
+
+
 # --------------------------------------------------------------------------
 # a5: append (EXT vLLM reshape_and_cache_flash, reached from worker.py:517-523)
 # --------------------------------------------------------------------------

@@ -157,3 +157,27 @@ def test_attention_argument_checks_and_workspace_size(lib):
     assert attn(max_len=4096, max_blocks=256, nwg=1, wsp=p, wsb=need - 1) == WS
     raw2, mis = _buf(64, misalign=4)
     assert attn(q=mis) == MISALIGNED
+
+
+def test_prepare_inputs_host_checks(lib):
+    """Argument errors are found on the host, before any device work."""
+    raw, p = _buf(1 << 12)
+    i32 = lambda xs: np.asarray(xs, dtype=np.int32)  # noqa: E731
+    i64 = lambda xs: np.asarray(xs, dtype=np.int64)  # noqa: E731
+
+    def prep(ids, offs, seq, ctx, n_query, batch=None, pad=4, bs=16):
+        ids, offs, seq, ctx = i32(ids), i64(offs), i32(seq), i32(ctx)
+        toks = i64(np.zeros(max(n_query, 1)))
+        b = len(seq) if batch is None else batch
+        return lib.aegkv_prepare_inputs(ids.ctypes.data if ids.size else None, offs.ctypes.data,
+                                        seq.ctypes.data, ctx.ctypes.data, toks.ctypes.data, b,
+                                        bs, pad, p, p, p, p, p, p, p, p, n_query, None)
+
+    assert prep([1], [0, 1], [5], [6], 0) == INVALID          # context_len > seq_len
+    assert prep([1], [0, 1], [17], [16], 1) == RANGE   # position 16 needs a 2nd block
+    assert prep([1, 2], [0, 2], [17], [16], 2) == INVALID     # query tokens must total 1
+    assert prep([1, 2], [0, 2], [17], [16], 1, pad=1) == INVALID  # decode table wider than pad
+    assert prep([-1], [0, 1], [3], [0], 3) == RANGE    # negative block id
+    assert prep([1], [1, 1], [3], [0], 3) == INVALID          # offsets must start at 0
+    assert prep([], [0], [], [], 0, batch=0) == OK
+    assert prep([1], [0, 1], [3], [0], 3, bs=0) == INVALID

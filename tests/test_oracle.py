@@ -235,3 +235,20 @@ def test_defrag_plan_invariants(seed):
         assert [pool[x] for x in old] == [moved[x] for x in nw]
     # already-dense pools move nothing
     assert ko.plan_defrag(valid[:30], valid) == ([], [])
+
+
+def test_prepare_model_inputs_literal():
+    """worker.py:596-676 on a prefill + two decodes, values worked by hand:
+    slot = table[p // 16] * 16 + p % 16; prefill rows of the padded table
+    are empty; start offsets are prefix sums."""
+    reqs = [(0, [11, 12, 13], 3, 0), (1, [7], 18, 17), (2, [9], 33, 32)]
+    r = ko.prepare_model_inputs(reqs, [[5], [2, 9], [4, 6, 8]])
+    assert r["slot_mapping"].tolist() == [80, 81, 82, 9 * 16 + 1, 8 * 16]
+    assert r["input_positions"].tolist() == [0, 1, 2, 17, 32]
+    assert r["input_tokens"].tolist() == [11, 12, 13, 7, 9]
+    assert r["block_tables"].tolist() == [[0, 0, 0], [2, 9, 0], [4, 6, 8]]
+    assert r["block_tables"].dtype == np.int32 and r["slot_mapping"].dtype == np.int64
+    assert r["query_start_loc"].tolist() == [0, 3, 4, 5]
+    assert r["seq_start_loc"].tolist() == [0, 3, 21, 54]
+    assert (r["num_prefills"], r["num_prefill_tokens"], r["num_decode_tokens"]) == (1, 3, 2)
+    assert (r["max_query_len"], r["max_prefill_seq_len"], r["max_decode_seq_len"]) == (3, 3, 33)
