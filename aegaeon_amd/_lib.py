@@ -52,7 +52,26 @@ SIGNATURES: Dict[str, tuple] = {
                                              c_void_p, c_int32, c_int32, c_int32, c_int32,
                                              c_int32, c_int32, c_float, c_int32, c_int32,
                                              c_void_p, c_uint64, c_void_p]),
+    # block manager (host bookkeeping)
+    "aegkv_bm_create": (c_int, [c_int64, c_int64, POINTER(c_void_p)]),
+    "aegkv_bm_destroy": (None, [c_void_p]),
+    "aegkv_bm_set_wait": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "aegkv_bm_define_shape": (c_int, [c_void_p, c_int32, c_uint64]),
+    "aegkv_bm_register_gpu_space": (c_int, [c_void_p, c_int32, c_int64, c_int32]),
+    "aegkv_bm_allocate": (c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_int64]),
+    "aegkv_bm_free": (c_int, [c_void_p, c_int64]),
+    "aegkv_bm_move": (c_int, [c_void_p, c_void_p, c_int64, c_int32, _i64p, _i64p, _i32p, _i32p]),
+    "aegkv_bm_move_ids": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
+                                  _i64p]),
+    "aegkv_bm_complete_moves": (c_int, [c_void_p, c_int32, c_int32, c_int64]),
+    "aegkv_bm_table": (c_int, [c_void_p, c_int64, _i32p, _i32p, _i64p, c_void_p, c_int64]),
+    "aegkv_bm_flat_tables": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64]),
+    "aegkv_bm_stats": (c_int, [c_void_p, c_int32, c_int32, _i64p, _i64p, _i64p, _i64p]),
+    "aegkv_bm_free_list": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_int64, _i64p]),
 }
+
+# int (*)(void* ctx, int32_t location, int32_t shape, int64_t serial)
+BM_WAIT_FN = ctypes.CFUNCTYPE(c_int, c_void_p, c_int32, c_int32, c_int64)
 
 
 class AegkvError(RuntimeError):

@@ -19,7 +19,10 @@ ROOT = PKG.parent
 BUILD_DIR = ROOT / "_build"
 LIB_PATH = PKG / "libaegkv.so"
 
-SOURCES = ["runtime.hip", "blocks.hip", "append.hip", "attention.hip", "inputs.hip"]
+SOURCES = [
+    "runtime.hip", "blocks.hip", "append.hip", "attention.hip", "inputs.hip",
+    "block_manager.cpp",
+]
 ARCH = "gfx950"
 
 # Packed FP32 instructions are disabled for every HIP translation unit.
@@ -43,10 +46,14 @@ def _hipcc() -> str:
 
 def _compile(src: str) -> Path:
     obj = BUILD_DIR / (Path(src).stem + ".o")
-    cmd = [_hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    if src.endswith(".cpp"):
+        # host-only bookkeeping: plain C++, no device code
+        cmd = ["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-c", str(CSRC / src), "-o", str(obj)]
+    else:
+        cmd = [_hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")
+        raise RuntimeError(f"compile failed for {src}:\n{res.stdout}\n{res.stderr}")
     return obj
 
 

@@ -147,6 +147,8 @@ const char* aegkv_strerror(int code) {
     case AEGKV_ERR_UNSUPPORTED: return "aegkv: unsupported shape or dtype";
     case AEGKV_ERR_WORKSPACE: return "aegkv: workspace or staging buffer too small";
     case AEGKV_ERR_RUNTIME: return "aegkv: a HIP runtime query failed while sizing the call";
+    case AEGKV_ERR_NO_SPACE: return "aegkv: not enough free blocks after reclaiming moves";
+    case AEGKV_ERR_IN_USE: return "aegkv: request lives elsewhere, or the space still holds requests";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);

@@ -226,6 +226,81 @@ int aegkv_prepare_inputs(const int32_t* block_ids, const int64_t* table_offsets,
                          int32_t* seq_start_loc_out, int64_t n_query_tokens,
                          aegkv_stream_t stream);
 
+/* ---- a8: node-wide block manager (host bookkeeping) ----------------------
+ * Replaces the allocation and move bookkeeping of BlockManager
+ * (aegaeon/aegaeon/block_manager.py:180-874).  Pure host code, no HIP calls;
+ * not thread-safe (one caller at a time, as the reference's event loop).
+ * Same id order as the reference, so the swap lists it produces are the
+ * reference's:
+ *   - per GPU engine a FIFO free list: allocations take from the head, frees
+ *     and reclaimed move sources go to the tail (:515-526,703,250-258);
+ *   - the CPU pool is num_slabs slabs of slab_bytes; a slab holds blocks of one
+ *     shape while any is used; per-shape free deques, a stack of free slabs and
+ *     per-slab usage counts (:186-199,528-580), slab reclaim (:474-496);
+ *     block ids of a shape are byte offsets / block_bytes (:242-245).
+ * A shape is a caller-chosen id (>= 0) with its block bytes.  Locations: an
+ * engine id >= 0 or AEGKV_BM_CPU.  When an allocation runs short, the pending
+ * moves out of that location are completed as _reclaim_gpu/cpu_move_blocks
+ * do (:410-472): the wait callback is called with the highest pending serial,
+ * returns 0 once every move up to it has finished copying, and their source
+ * blocks are reclaimed; without a callback, or when it returns non-zero, the
+ * call fails with AEGKV_ERR_NO_SPACE (the reference's ResourceWarning). */
+#define AEGKV_ERR_NO_SPACE (-9)      /* not enough free blocks after reclaim     */
+#define AEGKV_ERR_IN_USE (-10)       /* request lives elsewhere / space occupied  */
+#define AEGKV_BM_CPU (-1)            /* BLOCK_LOCATION_CPU (block_manager.py:96)  */
+
+typedef struct aegkv_block_manager aegkv_block_manager;
+typedef int (*aegkv_bm_wait_fn)(void* ctx, int32_t location, int32_t shape, int64_t serial);
+
+/* BlockManager.__init__ (:180-246): num_slabs CPU slabs of slab_bytes. */
+int aegkv_bm_create(int64_t cpu_num_slabs, int64_t cpu_slab_bytes, aegkv_block_manager** out);
+void aegkv_bm_destroy(aegkv_block_manager* bm);
+int aegkv_bm_set_wait(aegkv_block_manager* bm, aegkv_bm_wait_fn fn, void* ctx);
+/* Shape id -> bytes per block (_get_block_size_bytes, :239-240); fixed once set. */
+int aegkv_bm_define_shape(aegkv_block_manager* bm, int32_t shape, uint64_t block_bytes);
+/* register_gpu_space (:300-348): fresh free list [0, num_max_blocks); CPU
+ * moves into the replaced space are reclaimed.  AEGKV_ERR_IN_USE while a
+ * request still lives in it.  Only this engine's pending moves are dropped
+ * (the reference drops every engine's, stranding their source blocks). */
+int aegkv_bm_register_gpu_space(aegkv_block_manager* bm, int32_t engine, int64_t num_max_blocks,
+                                int32_t shape);
+/* allocate_blocks_batched (:651-694): request i ends with num_blocks_needed[i]
+ * blocks on `engine`; one batched allocation handed out in request order. */
+int aegkv_bm_allocate(aegkv_block_manager* bm, int32_t engine, const int64_t* request_ids,
+                      const int64_t* num_blocks_needed, int64_t n);
+/* free_blocks (:696-711). */
+int aegkv_bm_free(aegkv_block_manager* bm, int64_t request_id);
+/* move_requests (:778-874), CPU<->GPU: requests already at `target` are
+ * skipped, the others share location and shape.  Outputs the move's serial
+ * (-1: nothing moved), block count, direction and GPU engine; the id lists
+ * and the moved requests (first occurrences, in order; may be NULL) are read
+ * with aegkv_bm_move_ids before the next move.  A failed call changes
+ * no table (the reference leaves the earlier requests of the batch moved). */
+int aegkv_bm_move(aegkv_block_manager* bm, const int64_t* request_ids, int64_t n,
+                  int32_t target, int64_t* serial, int64_t* n_blocks, int32_t* is_swap_in,
+                  int32_t* engine);
+int aegkv_bm_move_ids(const aegkv_block_manager* bm, int64_t* src_ids, int64_t* dst_ids,
+                      int64_t cap, int64_t* moved_request_ids, int64_t request_cap,
+                      int64_t* n_moved);
+/* Reclaim the moves out of `location` (CPU: of `shape`) up to up_to_serial,
+ * whose copies the caller has seen finish (_reclaim_blocks, :360-408). */
+int aegkv_bm_complete_moves(aegkv_block_manager* bm, int32_t location, int32_t shape,
+                            int64_t up_to_serial);
+/* get_block_table (:718-721); blocks may be NULL to query the length. */
+int aegkv_bm_table(const aegkv_block_manager* bm, int64_t request_id, int32_t* location,
+                   int32_t* shape, int64_t* n_blocks, int64_t* blocks, int64_t cap);
+/* Tables of request_ids flattened for aegkv_prepare_inputs: offsets[n + 1],
+ * ids (int32, may be NULL to size). */
+int aegkv_bm_flat_tables(const aegkv_block_manager* bm, const int64_t* request_ids, int64_t n,
+                         int64_t* offsets, int32_t* ids, int64_t cap);
+/* log_block_usage counters (:730-768): free/moving blocks of an engine, or of
+ * a CPU shape with its slab count and used blocks. */
+int aegkv_bm_stats(const aegkv_block_manager* bm, int32_t location, int32_t shape,
+                   int64_t* n_free, int64_t* n_moving, int64_t* n_slabs, int64_t* n_used);
+/* The free list of an engine or a CPU shape, in allocation order. */
+int aegkv_bm_free_list(const aegkv_block_manager* bm, int32_t location, int32_t shape,
+                       int64_t* out, int64_t cap, int64_t* n);
+
 #ifdef __cplusplus
 }
 #endif
