@@ -27,7 +27,9 @@ attention (Qwen2.5-7B GQA 28/4, 128 sequences, lognormal mean 1500, up to 8192
 tokens) in us per layer; block pack and scatter for the Llama-2-13B swap
 workload (32 x 2048 tokens, 4096 blocks of 12.5 MiB) plus a sampled PCIe leg to
 pinned host; defrag of the unified multi-model pool followed by a Yi-1.5-9B
-decode step (append + attention); token gather.
+decode step (append + attention); token gather; device-side input preparation
+against the reference's host loops; the block manager's host bookkeeping
+(native against the reference's algorithm, same block ids).
 
 The CPU baseline is the numpy oracle's append timed on the host on a bounded
 sample of the same workload.
@@ -405,6 +407,59 @@ def bench_prepare(args, timer):
     return out
 
 
+# ------------------------------------------------------------------- block manager
+BM_POOL_BLOCKS = 200_000           # 175 GiB of 0.875 MiB Qwen2.5-7B blocks on one GPU
+BM_CPU_SLABS, BM_SLAB_BYTES = 128, 1 << 30   # aegaeon/aegaeon/config.py:37-39
+
+
+def bench_block_manager(args, timer):
+    """Host bookkeeping of one Qwen2.5-7B engine: a 200k-block GPU pool, the
+    reference's CPU pool of 128 x 1 GiB slabs, 256 running requests
+    (lognormal context mean 600).  A decode step grows every request by one
+    token and calls allocate_blocks_batched on the batch
+    (stage_engine.py:590); a turn moves the batch out to the CPU and back in
+    (decode_scheduler.py:154,225).  Native manager vs the oracle's
+    restatement of the reference's algorithm, same sequence, same ids."""
+    from aegaeon_amd.block_manager import BLOCK_LOCATION_CPU, BlockManager
+    from aegaeon_amd.workloads import QWEN25_7B, lognormal_lengths
+    from oracle.block_manager_oracle import BlockManagerOracle
+    shape = QWEN25_7B.block_shape
+    rng = np.random.default_rng(args.seed)
+    ctx = lognormal_lengths(rng, 256, 600.0, 1.0, 16, 4096)
+    rids = list(range(256))
+    n_steps, n_turns = 48, 3
+
+    def needed(step):
+        return [(int(c) + step + 1 + 15) // 16 for c in ctx]
+
+    def run(make, alloc, move, steps, turns):
+        m = make()
+        m.register_gpu_space(0, BM_POOL_BLOCKS, shape)
+        alloc(m, needed(0))
+        t0 = time.perf_counter()
+        for s in range(1, steps + 1):
+            alloc(m, needed(s))
+        t_step = (time.perf_counter() - t0) / steps
+        t0 = time.perf_counter()
+        for _ in range(turns):
+            move(m, BLOCK_LOCATION_CPU)
+            move(m, 0)
+        t_turn = (time.perf_counter() - t0) / turns
+        return m, t_step, t_turn
+
+    nat, ns, nt = run(lambda: BlockManager(BM_CPU_SLABS, BM_SLAB_BYTES),
+                      lambda m, need: m.allocate_blocks_by_count(rids, need, 0),
+                      lambda m, loc: m.move_request_ids(rids, loc), n_steps, n_turns)
+    ref, rs, rt = run(lambda: BlockManagerOracle(BM_CPU_SLABS, BM_SLAB_BYTES),
+                      lambda m, need: m.allocate_blocks_batched(list(zip(rids, need)), 0),
+                      lambda m, loc: m.move_requests(rids, loc), n_steps, n_turns)
+    same = all(nat.get_block_table(r).blocks == ref.block_tables[r].blocks for r in rids)
+    return {"native_us_per_step": ns * 1e6, "reference_us_per_step": rs * 1e6,
+            "native_ms_per_turn": nt * 1e3, "reference_ms_per_turn": rt * 1e3,
+            "blocks_per_turn": 2 * sum(len(ref.block_tables[r].blocks) for r in rids),
+            "same_ids": same}
+
+
 # ------------------------------------------------------------------ copy calibration
 CALIB_BLOCKS, CALIB_BLOCK_BYTES = 256, 1 << 20
 
@@ -499,7 +554,8 @@ def main(argv=None):
     p.add_argument("--swap-seqs", type=int, default=32)
     p.add_argument("--pcie-blocks", type=int, default=64)
     p.add_argument("--only", default="all",
-                   help="comma list of append,attention,pack,defrag,gather,prepare,calib or 'all'")
+                   help="comma list of append,attention,pack,defrag,gather,prepare,bm,calib "
+                        "or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU and "
@@ -514,13 +570,14 @@ def main(argv=None):
     torch.cuda.set_device(0)
     log(f"device: {torch.cuda.get_device_name(0)}")
     only = set(args.only.split(",")) if args.only != "all" else \
-        {"append", "attention", "pack", "defrag", "gather", "prepare", "calib"}
+        {"append", "attention", "pack", "defrag", "gather", "prepare", "bm", "calib"}
     timer = Timer()
     log(f"spin calibration: {timer.cycles_per_ms:.0f} cycles/ms")
     res = {}
     for name, fn in (("append", bench_append), ("attention", bench_attention),
                      ("gather", bench_gather), ("pack", bench_pack), ("defrag", bench_defrag),
-                     ("prepare", bench_prepare), ("calib", bench_calib)):
+                     ("prepare", bench_prepare), ("bm", bench_block_manager),
+                     ("calib", bench_calib)):
         if name in only:
             t0 = time.perf_counter()
             res[name] = fn(args, timer)
@@ -600,6 +657,17 @@ def main(argv=None):
         ops_out["prepare_inputs_us_per_step"] = {
             k: {"device": round(v["device"], 1), "reference_host_loops": round(v["reference_host"], 1)}
             for k, v in res["prepare"].items()}
+    if "bm" in res:
+        b = res["bm"]
+        ops_out["block_manager"] = {
+            "workload": "Qwen2.5-7B engine, 200k-block GPU pool, 128 x 1 GiB CPU slabs, 256 "
+                        "requests; step = allocate_blocks_batched after one token each, turn = "
+                        "batch moved out to CPU and back in",
+            "native_us_per_step": round(b["native_us_per_step"], 1),
+            "reference_algorithm_us_per_step": round(b["reference_us_per_step"], 1),
+            "native_ms_per_turn": round(b["native_ms_per_turn"], 3),
+            "reference_algorithm_ms_per_turn": round(b["reference_ms_per_turn"], 3),
+            "blocks_moved_per_turn": b["blocks_per_turn"], "same_block_ids": b["same_ids"]}
     if "calib" in res:
         c = res["calib"]
         cg = c["bytes"] / (c["ms"] * 1e-3) / 1e9
