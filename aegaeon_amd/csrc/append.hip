@@ -40,8 +40,8 @@ struct AppendArgs {
 // keeps the dependent-latency chain at one HBM round trip plus the store.
 // One chunk per lane in 64-lane workgroups (a wave per 1 KiB row at the
 // Qwen2.5-7B shape) measured fastest on MI355X: the step is a single burst of
-// loads and stores, and spreading it over the most workgroups (3584 for the
-// 256-token x 28-layer step, 128 for one layer) shortens the burst; 2-8
+// loads and stores, and spreading it over the most workgroups (14336 for the
+// 256-token x 28-layer step, 512 for one layer) shortens the burst; 2-8
 // chunks per lane and 256-512-lane workgroups were 2-65% slower.  The K/V
 // rows are read once and the cache rows are not read again before the
 // attention of the step streams them, so both sides are non-temporal.
