@@ -52,6 +52,10 @@ SIGNATURES: Dict[str, tuple] = {
                                              c_void_p, c_int32, c_int32, c_int32, c_int32,
                                              c_int32, c_int32, c_float, c_int32, c_int32,
                                              c_void_p, c_uint64, c_void_p]),
+    "aegkv_varlen_prefill_attention": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                               c_int64, c_void_p, c_int64, c_void_p, c_int32,
+                                               c_int32, c_int64, c_int32, c_int32, c_int32,
+                                               c_float, c_int32, c_int32, c_void_p]),
     # block manager (host bookkeeping)
     "aegkv_bm_create": (c_int, [c_int64, c_int64, POINTER(c_void_p)]),
     "aegkv_bm_destroy": (None, [c_void_p]),

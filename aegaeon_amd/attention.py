@@ -7,7 +7,9 @@ its model forward (aegaeon/aegaeon/worker.py:517-523):
   ``[N, L, 2, 16, Hkv, D]`` storage (worker.py:389-395) in one launch;
 * :func:`gather_tokens` — block-table de-page into contiguous buffers;
 * :func:`flash_attn_with_kvcache` — vllm-flash-attn's paged decode call
-  (selected at worker.py:410-418) for one query token per sequence.
+  (selected at worker.py:410-418) for one query token per sequence;
+* :func:`flash_attn_varlen_func` — vllm-flash-attn's varlen call of the
+  backend's prompt run (causal attention of packed prompts).
 
 All of them enqueue hand-written gfx950 kernels on the current torch stream.
 """
@@ -254,3 +256,63 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     o = paged_decode_attention(q.view(B, Hq, D), k_cache, v_cache, block_table, cache_seqlens,
                                scale, ms, out=None if out is None else out.view(B, Hq, D))
     return o.view(B, 1, Hq, D)
+
+
+def varlen_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                             cu_seqlens: torch.Tensor, max_seqlen: int, scale: float,
+                             causal: bool = True, out: Optional[torch.Tensor] = None
+                             ) -> torch.Tensor:
+    """Attention of packed sequences: ``q [T, Hq, D]``, ``k, v [T, Hkv, D]``
+    (any token stride, dense heads), sequence b = tokens
+    ``cu_seqlens[b] .. cu_seqlens[b+1]`` (int32 on the GPU).  Returns
+    ``out [T, Hq, D]``.  ``max_seqlen`` is the host bound of the lengths."""
+    for x, n in ((q, "q"), (k, "k"), (v, "v")):
+        if x.dim() != 3:
+            raise ValueError(f"{n} must be [tokens, heads, head_dim]")
+        _check_rows(x, n)
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share a bf16/fp16 dtype")
+    T, Hq, D = q.shape
+    if k.shape != v.shape or k.size(0) != T or k.size(2) != D:
+        raise ValueError("k and v must be [tokens, Hkv, D] with q's tokens and head_dim")
+    if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_cuda or cu_seqlens.dim() != 1 \
+            or not cu_seqlens.is_contiguous():
+        raise ValueError("cu_seqlens must be a contiguous int32 GPU tensor [batch + 1]")
+    if out is None:
+        out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
+    elif out.shape != (T, Hq, D) or out.dtype != q.dtype:
+        raise ValueError("out must be [tokens, Hq, D] of q's dtype")
+    else:
+        _check_rows(out, "out")
+    with torch.cuda.device(q.device):
+        rc = _lib.load().aegkv_varlen_prefill_attention(
+            out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0),
+            v.data_ptr(), v.stride(0), cu_seqlens.data_ptr(), cu_seqlens.numel() - 1,
+            int(max_seqlen), T, Hq, k.size(1), D, float(scale), int(bool(causal)),
+            _DTYPES[q.dtype], _stream(q))
+    _lib.check(rc, "varlen_prefill_attention")
+    return out
+
+
+def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                           max_seqlen_q: int, max_seqlen_k: int, dropout_p: float = 0.0,
+                           softmax_scale: Optional[float] = None, causal: bool = False,
+                           window_size: Tuple[int, int] = (-1, -1), alibi_slopes=None,
+                           deterministic: bool = False, return_attn_probs: bool = False,
+                           block_table: Optional[torch.Tensor] = None,
+                           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """vllm-flash-attn's varlen call as the FlashAttention backend makes it for
+    a prompt run without cached prefix: the same ``cu_seqlens`` for queries
+    and keys.  Dropout, sliding windows, ALiBi, attention probabilities and a
+    paged prefix raise NotImplementedError (the reference's models use none)."""
+    if dropout_p != 0.0 or tuple(window_size) != (-1, -1) or alibi_slopes is not None \
+            or return_attn_probs or block_table is not None:
+        raise NotImplementedError("only the plain (causal) prompt run is supported")
+    if cu_seqlens_k is not cu_seqlens_q and not torch.equal(cu_seqlens_k, cu_seqlens_q):
+        raise NotImplementedError("queries and keys must share cu_seqlens (no cached prefix)")
+    if max_seqlen_k != max_seqlen_q:
+        raise NotImplementedError("queries and keys must share max_seqlen")
+    D = q.size(-1)
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    return varlen_prefill_attention(q, k, v, cu_seqlens_q, max_seqlen_q, scale, causal, out)

@@ -226,6 +226,25 @@ int aegkv_prepare_inputs(const int32_t* block_ids, const int64_t* table_offsets,
                          int32_t* seq_start_loc_out, int64_t n_query_tokens,
                          aegkv_stream_t stream);
 
+/* ---- prefill-side attention (EXT flash_attn_varlen_func) -----------------
+ * The prompt run of vLLM 0.5.1's FlashAttention backend, reached from
+ * aegaeon/aegaeon/worker.py:517-523 with cu_seqlens = seq_start_loc and
+ * max_seqlen = max_prefill_seq_len (worker.py:652-711).  q [total, Hq, D],
+ * k and v [total, Hkv, D], out [total, Hq, D] (DEVICE, 16-bit, token strides
+ * in elements, the heads of a token contiguous, 16-byte aligned).  Sequence b
+ * holds tokens [cu_seqlens[b], cu_seqlens[b+1]) (DEVICE int32 [batch + 1]);
+ * query i of a sequence attends to keys j <= i of it (every key when causal
+ * is 0), softmax(scale * q.k) in fp32 with P rounded to 16 bits before P.V.
+ * Lengths are clamped to max_seqlen (the host bound that sizes the grid) and
+ * tokens to [0, total_tokens).  head_dim 64 or 128, Hq a multiple of Hkv. */
+int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const void* q,
+                                   int64_t q_token_stride, const void* k, int64_t k_token_stride,
+                                   const void* v, int64_t v_token_stride,
+                                   const int32_t* cu_seqlens, int32_t batch, int32_t max_seqlen,
+                                   int64_t total_tokens, int32_t n_q_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, float scale, int32_t causal, int32_t dtype,
+                                   aegkv_stream_t stream);
+
 /* ---- a8: node-wide block manager (host bookkeeping) ----------------------
  * Replaces the allocation and move bookkeeping of BlockManager
  * (aegaeon/aegaeon/block_manager.py:180-874).  Pure host code, no HIP calls;

@@ -266,3 +266,40 @@ def paged_decode_attention(q: np.ndarray, key_cache: np.ndarray, value_cache: np
         p /= p.sum(axis=-1, keepdims=True)
         out[b] = np.einsum("hgt,thd->hgd", p, v).reshape(Hq, D)
     return out
+
+
+# --------------------------------------------------------------------------
+# prefill: EXT flash_attn_varlen_func, the prompt run of vLLM's
+# FlashAttention backend (reached from worker.py:517-523; cu_seqlens =
+# seq_start_loc, worker.py:665-673)
+# --------------------------------------------------------------------------
+def varlen_prefill_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
+                             cu_seqlens: Sequence[int], scale: float,
+                             causal: bool = True) -> np.ndarray:
+    """Textbook softmax attention of packed sequences in float64.
+
+    q: ``[T, Hq, D]``, k/v: ``[T, Hkv, D]`` float; sequence b is tokens
+    ``cu_seqlens[b] .. cu_seqlens[b+1]``; query i of a sequence sees keys
+    ``j <= i`` of it when causal, all of them otherwise; query head h reads kv
+    head ``h // (Hq // Hkv)``.  Tokens outside every sequence stay 0.
+    """
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    out = np.zeros((T, Hq, D), dtype=np.float64)
+    for b in range(len(cu_seqlens) - 1):
+        s0, s1 = int(cu_seqlens[b]), int(cu_seqlens[b + 1])
+        n = s1 - s0
+        if n <= 0:
+            continue
+        qb = q[s0:s1].astype(np.float64).reshape(n, Hkv, G, D)
+        kb = k[s0:s1].astype(np.float64)
+        vb = v[s0:s1].astype(np.float64)
+        s = np.einsum("ihgd,jhd->hgij", qb, kb) * scale
+        if causal:
+            s = np.where(np.tril(np.ones((n, n), dtype=bool)), s, -np.inf)
+        s -= s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[s0:s1] = np.einsum("hgij,jhd->ihgd", p, vb).reshape(n, Hq, D)
+    return out

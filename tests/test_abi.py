@@ -181,3 +181,24 @@ def test_prepare_inputs_host_checks(lib):
     assert prep([1], [1, 1], [3], [0], 3) == INVALID          # offsets must start at 0
     assert prep([], [0], [], [], 0, batch=0) == OK
     assert prep([1], [0, 1], [3], [0], 3, bs=0) == INVALID
+
+
+def test_prefill_attention_host_checks(lib):
+    """Shapes, dtypes, strides and alignment are checked on the host."""
+    raw, p = _buf(1 << 12)
+
+    def call(q=p, out=p, qs=28 * 128, ks=4 * 128, os_=28 * 128, batch=1, ms=16, total=16,
+             hq=28, hkv=4, d=128, dt=0, scale=0.1):
+        return lib.aegkv_varlen_prefill_attention(out, os_, q, qs, p, ks, p, ks, p, batch, ms,
+                                                  total, hq, hkv, d, scale, 1, dt, None)
+
+    assert call(hq=28, hkv=5) == INVALID           # Hq not a multiple of Hkv
+    assert call(d=32) == UNSUP                      # head_dim 64 or 128 only
+    assert call(dt=7) == UNSUP
+    assert call(qs=27 * 128) == INVALID             # token row shorter than its heads
+    assert call(os_=28 * 128 + 4) == MISALIGNED     # stride not a multiple of 16 bytes
+    assert call(q=p + 2) == MISALIGNED
+    assert call(scale=float("nan")) == INVALID
+    assert call(batch=0, q=None, out=None) == OK    # nothing to do
+    assert call(ms=0) == OK
+    assert call(q=None) == INVALID

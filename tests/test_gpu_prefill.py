@@ -1,0 +1,179 @@
+"""GPU parity of the varlen prefill attention (EXT flash_attn_varlen_func, the
+prompt run reached from aegaeon/aegaeon/worker.py:517-523) against the
+oracle's float64 textbook attention, through the C ABI.
+
+Tolerance: the kernel rounds P to 16 bits before P.V, as FlashAttention does,
+and rounds the output to the I/O dtype.  Against float64 the bar is a relative
+L2 error of 4e-3 (bf16) / 1e-3 (fp16) per call, and an elementwise error of at
+most 2^-6 (bf16) / 2^-8 (fp16) of the output's largest magnitude."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from aegaeon_amd import attention as A
+from aegaeon_amd._lib import AegkvError
+from oracle import kv_oracle as ko
+
+pytestmark = pytest.mark.gpu
+
+BARS = {torch.bfloat16: (4e-3, 2.0 ** -6), torch.float16: (1e-3, 2.0 ** -8)}
+
+
+def _packed(lens, Hq, Hkv, D, dtype, seed, extra=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1]) + extra
+    q = torch.randn((T, Hq, D), generator=g, device="cuda").to(dtype)
+    k = torch.randn((T, Hkv, D), generator=g, device="cuda").to(dtype)
+    v = torch.randn((T, Hkv, D), generator=g, device="cuda").to(dtype)
+    return cu, q, k, v
+
+
+def _check(got, q, k, v, cu, scale, causal, dtype, n_tokens=None):
+    torch.cuda.synchronize()
+    n = int(cu[-1]) if n_tokens is None else n_tokens
+    ref = ko.varlen_prefill_attention(q[:n].double().cpu().numpy(), k[:n].double().cpu().numpy(),
+                                      v[:n].double().cpu().numpy(), cu, scale, causal)
+    out = got[:n].double().cpu().numpy()
+    assert np.isfinite(out).all()
+    rel, elem = BARS[dtype]
+    err = np.linalg.norm(out - ref) / max(np.linalg.norm(ref), 1e-30)
+    worst = np.abs(out - ref).max() / max(np.abs(ref).max(), 1e-30)
+    assert err <= rel, (err, worst)
+    assert worst <= elem, (err, worst)
+    return err
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(28, 4, 128), (8, 8, 64), (16, 2, 128), (12, 3, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_ragged_batch_matches_oracle(Hq, Hkv, D, causal):
+    lens = [1, 15, 16, 17, 63, 64, 65, 127, 128, 129, 300]
+    cu, q, k, v = _packed(lens, Hq, Hkv, D, torch.bfloat16, Hq + D)
+    scale = 1.0 / math.sqrt(D)
+    cu_t = torch.from_numpy(cu).cuda()
+    out = A.varlen_prefill_attention(q, k, v, cu_t, max(lens), scale, causal)
+    _check(out, q, k, v, cu, scale, causal, torch.bfloat16)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp16(D):
+    lens = [200, 7, 129]
+    cu, q, k, v = _packed(lens, 8, 2, D, torch.float16, 5)
+    cu_t = torch.from_numpy(cu).cuda()
+    out = A.varlen_prefill_attention(q, k, v, cu_t, max(lens), 0.1, True)
+    _check(out, q, k, v, cu, 0.1, True, torch.float16)
+
+
+def test_strided_views_of_fused_qkv():
+    """q, k, v as column slices of one [T, (Hq + 2 Hkv) D] projection output,
+    out as a slice of a wider buffer: token strides differ from the rows."""
+    Hq, Hkv, D = 28, 4, 128
+    lens = [33, 190, 64]
+    T = sum(lens)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    qkv = torch.randn((T, (Hq + 2 * Hkv) * D), generator=g, device="cuda").to(torch.bfloat16)
+    q = qkv[:, :Hq * D].view(T, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D)
+    v = qkv[:, (Hq + Hkv) * D:].view(T, Hkv, D)
+    wide = torch.full((T, Hq * D + 64), 7.0, device="cuda", dtype=torch.bfloat16)
+    out = wide[:, :Hq * D].view(T, Hq, D)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), max(lens), 0.088, True,
+                               out=out)
+    _check(out, q, k, v, cu, 0.088, True, torch.bfloat16)
+    assert bool((wide[:, Hq * D:] == 7.0).all())
+
+
+def test_empty_sequences_loose_bound_and_nan_padding():
+    """Zero-length sequences, a host bound above every length, and NaN rows
+    after the last sequence (padding tokens): the outputs of real tokens are
+    right and padding rows of out are not written."""
+    lens = [0, 40, 0, 130, 1]
+    cu, q, k, v = _packed(lens, 4, 2, 64, torch.bfloat16, 3, extra=24)
+    n = int(cu[-1])
+    for x in (q, k, v):
+        x[n:] = float("nan")
+    out = torch.full_like(q, 3.0)
+    A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), 400, 0.125, True, out=out)
+    _check(out, q, k, v, cu, 0.125, True, torch.bfloat16)
+    assert bool((out[n:] == 3.0).all())
+
+
+def test_lengths_clamped_to_host_bound():
+    """A device length above max_seqlen is clamped to it, never read past."""
+    lens = [100, 50]
+    cu, q, k, v = _packed(lens, 4, 4, 64, torch.bfloat16, 8)
+    out = torch.zeros_like(q)
+    A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), 64, 0.125, True, out=out)
+    torch.cuda.synchronize()
+    # sequence 0 is processed as its first 64 tokens; sequence 1 (50) in full
+    ref0 = ko.varlen_prefill_attention(q[:64].double().cpu().numpy(),
+                                       k[:64].double().cpu().numpy(),
+                                       v[:64].double().cpu().numpy(), [0, 64], 0.125, True)
+    got = out.double().cpu().numpy()
+    assert np.abs(got[:64] - ref0).max() <= 2.0 ** -6 * np.abs(ref0).max()
+    assert not got[64:100].any()
+    _check(out[100:], q[100:], k[100:], v[100:], np.array([0, 50], dtype=np.int32), 0.125,
+           True, torch.bfloat16)
+
+
+def test_deterministic():
+    lens = [300, 77]
+    cu, q, k, v = _packed(lens, 28, 4, 128, torch.bfloat16, 12)
+    cu_t = torch.from_numpy(cu).cuda()
+    a = A.varlen_prefill_attention(q, k, v, cu_t, 300, 0.088, True)
+    b = A.varlen_prefill_attention(q, k, v, cu_t, 300, 0.088, True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def _torch_reference(q, k, v, cu, scale):
+    """float32 causal attention on the GPU, one sequence at a time (operands
+    made contiguous before every product)."""
+    T, Hq, D = q.shape
+    G = Hq // k.size(1)
+    out = torch.zeros((T, Hq, D), dtype=torch.float32, device=q.device)
+    for b in range(len(cu) - 1):
+        s0, s1 = int(cu[b]), int(cu[b + 1])
+        n = s1 - s0
+        qf = q[s0:s1].float().transpose(0, 1).contiguous()
+        kf = k[s0:s1].float().transpose(0, 1).repeat_interleave(G, 0)
+        vf = v[s0:s1].float().transpose(0, 1).repeat_interleave(G, 0).contiguous()
+        s = torch.bmm(qf, kf.transpose(1, 2).contiguous()) * scale
+        s.masked_fill_(torch.ones((n, n), dtype=torch.bool, device=q.device).triu(1), -math.inf)
+        p = torch.softmax(s, dim=-1)
+        out[s0:s1] = torch.bmm(p, vf).transpose(0, 1)
+    return out
+
+
+def test_qwen_prompt_batch_full_size():
+    """Qwen2.5-7B prompt run, 4 prompts x 2048 tokens, GQA 28/4, D 128, bf16,
+    against float32 attention computed on the GPU."""
+    lens = [2048] * 4
+    cu, q, k, v = _packed(lens, 28, 4, 128, torch.bfloat16, 21)
+    scale = 1.0 / math.sqrt(128)
+    out = A.flash_attn_varlen_func(q, k, v, torch.from_numpy(cu).cuda(),
+                                   torch.from_numpy(cu).cuda(), 2048, 2048, softmax_scale=scale,
+                                   causal=True)
+    ref = _torch_reference(q, k, v, cu, scale)
+    torch.cuda.synchronize()
+    err = (out.float() - ref).norm() / ref.norm()
+    worst = (out.float() - ref).abs().max() / ref.abs().max()
+    assert float(err) <= 4e-3, float(err)
+    assert float(worst) <= 2.0 ** -6, float(worst)
+
+
+def test_wrapper_rejects_unsupported_options():
+    cu, q, k, v = _packed([10], 4, 4, 64, torch.bfloat16, 1)
+    cu_t = torch.from_numpy(cu).cuda()
+    with pytest.raises(NotImplementedError):
+        A.flash_attn_varlen_func(q, k, v, cu_t, cu_t, 10, 10, dropout_p=0.1)
+    with pytest.raises(NotImplementedError):
+        A.flash_attn_varlen_func(q, k, v, cu_t, cu_t, 10, 10, window_size=(4, 0))
+    with pytest.raises(NotImplementedError):
+        A.flash_attn_varlen_func(q, k, v, cu_t, cu_t, 10, 12)
+    with pytest.raises(AegkvError):
+        A.varlen_prefill_attention(q[:, :, :32].contiguous(), k[:, :, :32].contiguous(),
+                                   v[:, :, :32].contiguous(), cu_t, 10, 0.1)

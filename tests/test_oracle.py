@@ -252,3 +252,76 @@ def test_prepare_model_inputs_literal():
     assert r["seq_start_loc"].tolist() == [0, 3, 21, 54]
     assert (r["num_prefills"], r["num_prefill_tokens"], r["num_decode_tokens"]) == (1, 3, 2)
     assert (r["max_query_len"], r["max_prefill_seq_len"], r["max_decode_seq_len"]) == (3, 3, 33)
+
+
+# ---------------------------------------------------------------------------
+# varlen prefill attention
+# ---------------------------------------------------------------------------
+def _packed_case(rng, lens, Hq, Hkv, D):
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    q = rng.standard_normal((T, Hq, D))
+    k = rng.standard_normal((T, Hkv, D))
+    v = rng.standard_normal((T, Hkv, D))
+    return cu, q, k, v
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 16), (6, 2, 32), (7, 1, 8)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_matches_torch_sdpa_fp64(Hq, Hkv, D, causal):
+    """torch's own causal SDPA in float64, one sequence at a time, with the
+    kv heads repeated for GQA (head h reads kv head h // G)."""
+    rng = np.random.default_rng(Hq * 10 + D)
+    lens = [1, 5, 17, 33]
+    cu, q, k, v = _packed_case(rng, lens, Hq, Hkv, D)
+    scale = 0.3
+    got = ko.varlen_prefill_attention(q, k, v, cu, scale, causal)
+    G = Hq // Hkv
+    for b in range(len(lens)):
+        s0, s1 = cu[b], cu[b + 1]
+        qt = torch.from_numpy(q[s0:s1]).transpose(0, 1)               # [Hq, n, D]
+        kt = torch.from_numpy(k[s0:s1]).transpose(0, 1).repeat_interleave(G, 0)
+        vt = torch.from_numpy(v[s0:s1]).transpose(0, 1).repeat_interleave(G, 0)
+        want = torch.nn.functional.scaled_dot_product_attention(
+            qt.contiguous(), kt.contiguous(), vt.contiguous(), scale=scale, is_causal=causal)
+        np.testing.assert_allclose(got[s0:s1], want.transpose(0, 1).numpy(), rtol=1e-12,
+                                   atol=1e-12)
+
+
+def test_prefill_closed_forms():
+    """Causal: query 0 sees only key 0, so its output is v[0]; with equal keys
+    query i outputs the mean of v[0..i]; a dominant logit picks its value row."""
+    rng = np.random.default_rng(9)
+    cu, q, k, v = _packed_case(rng, [6, 9], 4, 2, 8)
+    out = ko.varlen_prefill_attention(q, k, v, cu, 0.5, True)
+    for b in range(2):
+        s0 = cu[b]
+        np.testing.assert_allclose(out[s0], np.repeat(v[s0], 2, axis=0), rtol=1e-14)
+    k_eq = np.broadcast_to(k[:1], k.shape).copy()
+    out = ko.varlen_prefill_attention(q, k_eq, v, cu, 0.5, True)
+    for b in range(2):
+        s0, s1 = cu[b], cu[b + 1]
+        for i in range(s1 - s0):
+            want = np.repeat(v[s0:s0 + i + 1].mean(axis=0), 2, axis=0)
+            np.testing.assert_allclose(out[s0 + i], want, rtol=1e-12, atol=1e-12)
+    out = ko.varlen_prefill_attention(q, k_eq, v, cu, 0.5, False)
+    np.testing.assert_allclose(out[cu[1] + 2], np.repeat(v[cu[1]:].mean(axis=0), 2, axis=0),
+                               rtol=1e-12, atol=1e-12)
+    k_dom = k.copy()
+    q1 = np.zeros_like(q)
+    q1[:, :, 0] = 1.0
+    k_dom[:, :, 0] = 0.0
+    k_dom[cu[1] + 3, :, 0] = 500.0                     # key 3 of sequence 1
+    out = ko.varlen_prefill_attention(q1, k_dom, v, cu, 1.0, True)
+    np.testing.assert_allclose(out[cu[1] + 7], np.repeat(v[cu[1] + 3], 2, axis=0), rtol=1e-12)
+    np.testing.assert_allclose(out[cu[1] + 2], np.repeat(v[cu[1]:cu[1] + 3].mean(axis=0), 2,
+                                                         axis=0), rtol=1e-12)
+
+
+def test_prefill_gqa_equals_mha_with_repeated_heads():
+    rng = np.random.default_rng(10)
+    cu, q, k, v = _packed_case(rng, [12, 3, 20], 6, 2, 16)
+    gqa = ko.varlen_prefill_attention(q, k, v, cu, 0.2, True)
+    mha = ko.varlen_prefill_attention(q, np.repeat(k, 3, axis=1), np.repeat(v, 3, axis=1), cu,
+                                      0.2, True)
+    np.testing.assert_allclose(gqa, mha, rtol=1e-12, atol=1e-14)
