@@ -11,7 +11,10 @@
 // Work: a workgroup of four waves takes 128 queries of one head of one
 // sequence; wave w owns queries [32w, 32w + 32).  Workgroups are numbered with
 // the query tile slowest, in decreasing order, so the most expensive tiles
-// (the last of each sequence) are dispatched first.
+// (the last of each sequence) are dispatched first; two fit on a CU.  (A
+// persistent grid dealing the same jobs in snake order measured 5% slower on
+// 4 x 2048 tokens and 60% slower on ragged batches, whose short sequences
+// leave most high-tile jobs empty.)
 //
 // Per 64-key tile, staged in LDS by the whole workgroup (two stages):
 //   S^T[64 keys x 32 queries] = K[64 x D] . Q^T[D x 32]   2 x D/16 MFMA 32x32x16
@@ -39,6 +42,9 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPfThreads = 256;
 constexpr int kPfQTile = 128;                // queries per workgroup
@@ -55,10 +61,9 @@ struct PfOps<AEGKV_DTYPE_BF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  // round to nearest even (finite x)
-  static __device__ __forceinline__ uint32_t to16(float x) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, x);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  // two floats to two 16-bit values, round to nearest even (one instruction)
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x, y}, bf16x2));
   }
 };
 
@@ -68,10 +73,18 @@ struct PfOps<AEGKV_DTYPE_FP16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t to16(float x) {
-    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x, y}, f16x2));
   }
 };
+
+// {lo16(a), lo16(b)} and {hi16(a), hi16(b)} (v_perm_b32: src1 = bytes 0-3)
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
 
 struct PrefillArgs {
   const uint8_t* q;
@@ -82,34 +95,24 @@ struct PrefillArgs {
   const int32_t* cu_seqlens;                   // [batch + 1], device
   int64_t total_tokens;
   int32_t batch, n_q_heads, group, max_seqlen, n_qtiles, causal;
-  float scale_log2;                            // softmax scale * log2(e)
+  float scale_log2;                            // softmax scale * log2(e), > 0
 };
 
+// Queries [q0, q0 + 128) of head h of the sequence at token s0 with len
+// tokens.
 template <int DT, int D>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(PrefillArgs a) {
+__device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, int h, int64_t s0,
+                                            int len, int q0) {
   using E = PfOps<DT>;
   constexpr int KPITCH = D * 2 + 16;            // bytes per K row in LDS
   constexpr int K_BYTES = kPfKTile * KPITCH;
-  constexpr int STAGE = K_BYTES + D * kVtPitch;
+  constexpr int V_BYTES = D * kVtPitch;
   constexpr int KS = D / 16;                    // k-steps of K.Q^T
   constexpr int DB = D / 32;                    // 32-row blocks of O^T
   constexpr int CPR = D / 8;                    // 16-byte chunks per row
   constexpr int KRPP = kPfThreads / CPR;        // K rows staged per pass
   constexpr int KPASS = kPfKTile / KRPP;
   constexpr int VTHREADS = (kPfKTile / 4) * CPR;  // (4-key quad, chunk) pairs
-  __shared__ __align__(16) uint8_t lds[2 * STAGE];
-
-  const int hb = a.n_q_heads * a.batch;
-  const int id = blockIdx.x;
-  const int tile = a.n_qtiles - 1 - id / hb;
-  const int h = (id % hb) / a.batch;
-  const int b = id % a.batch;
-  int64_t s0 = a.cu_seqlens[b], s1 = a.cu_seqlens[b + 1];
-  s0 = min(max(s0, (int64_t)0), a.total_tokens);
-  s1 = min(max(s1, s0), a.total_tokens);
-  const int len = (int)min(s1 - s0, (int64_t)a.max_seqlen);
-  const int q0 = tile * kPfQTile;
-  if (q0 >= len) return;  // uniform over the workgroup, before any barrier
   const int kvh = h / a.group;
   const int kv_end = a.causal ? min(len, q0 + kPfQTile) : len;
   const int n_kt = (kv_end + kPfKTile - 1) / kPfKTile;
@@ -117,6 +120,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(Prefil
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int col = lane & 31, hh = lane >> 5;
   const int qi = q0 + 32 * w + col;  // this lane's query, relative to the sequence
+  const int wq0 = q0 + 32 * w;       // the wave's first query
 
   // Q^T operand: query qi, dims 16 ks + 8 hh .. +7 (rows past the end are 0)
   u32x4 qv[KS];
@@ -135,46 +139,93 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(Prefil
   const int vq = t % (kPfKTile / 4), vc = t / (kPfKTile / 4);
   // position of the quad in the stored key order (quads 0, 2, 1, 3 of 16 keys)
   const int vpos = 16 * (vq >> 2) + 4 * (((vq & 1) << 1) | ((vq >> 1) & 1));
+  const uint32_t koff = (uint32_t)(kr * a.k_tok_b) + kc * 16;
+  const uint32_t voff = (uint32_t)(4 * vq * a.v_tok_b) + vc * 16;
   u32x4 kreg[KPASS], vreg[4];
 
-  auto load_tile = [&](int kt) {
+  auto load_k = [&](int kt) {
+    const int r0 = kt * kPfKTile;
+    if (r0 + kPfKTile <= len) {  // whole tile inside the sequence (uniform)
+      const uint8_t* kb = kbase + r0 * a.k_tok_b;
 #pragma unroll
-    for (int p = 0; p < KPASS; ++p) {
-      const int row = min(kt * kPfKTile + kr + KRPP * p, len - 1);
-      kreg[p] = *reinterpret_cast<const u32x4*>(kbase + row * a.k_tok_b + kc * 16);
+      for (int p = 0; p < KPASS; ++p)
+        kreg[p] = *reinterpret_cast<const u32x4*>(kb + p * KRPP * a.k_tok_b + koff);
+    } else {  // last tile: rows clamped to the sequence (masked in S)
+#pragma unroll
+      for (int p = 0; p < KPASS; ++p) {
+        const int row = min(r0 + kr + KRPP * p, len - 1);
+        kreg[p] = *reinterpret_cast<const u32x4*>(kbase + row * a.k_tok_b + kc * 16);
+      }
     }
-    if (t < VTHREADS) {
+  };
+  auto load_v = [&](int kt) {
+    if (t >= VTHREADS) return;
+    const int r0 = kt * kPfKTile;
+    if (r0 + kPfKTile <= len) {
+      const uint8_t* vb = vbase + r0 * a.v_tok_b;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        vreg[i] = *reinterpret_cast<const u32x4*>(vb + i * a.v_tok_b + voff);
+    } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = min(kt * kPfKTile + 4 * vq + i, len - 1);
+        const int row = min(r0 + 4 * vq + i, len - 1);
         vreg[i] = *reinterpret_cast<const u32x4*>(vbase + row * a.v_tok_b + vc * 16);
       }
     }
   };
-  auto store_tile = [&](int kt, uint8_t* st) {
+  auto store_k = [&](int slot) {
+    uint8_t* st = lds + slot * K_BYTES;
 #pragma unroll
     for (int p = 0; p < KPASS; ++p)
       *reinterpret_cast<u32x4*>(st + (kr + KRPP * p) * KPITCH + kc * 16) = kreg[p];
-    if (t < VTHREADS) {
-      u32x4 x[4];
+  };
+  auto store_v = [&](int kt, int slot) {
+    if (t >= VTHREADS) return;
+    u32x4 x[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)  // keys past the end: 0 (P is 0 there, V may be NaN)
-        x[i] = kt * kPfKTile + 4 * vq + i < len ? vreg[i] : u32x4{0, 0, 0, 0};
-      uint8_t* vt = st + K_BYTES + vpos * 2;
+    for (int i = 0; i < 4; ++i)  // keys past the end: 0 (P is 0 there, V may be NaN)
+      x[i] = kt * kPfKTile + 4 * vq + i < len ? vreg[i] : u32x4{0, 0, 0, 0};
+    uint8_t* vt = lds + 2 * K_BYTES + slot * V_BYTES + vpos * 2;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int sh = 16 * (e & 1), wd = e >> 1;
-        const uint32_t v0 = (x[0][wd] >> sh) & 0xffffu, v1 = (x[1][wd] >> sh) & 0xffffu;
-        const uint32_t v2 = (x[2][wd] >> sh) & 0xffffu, v3 = (x[3][wd] >> sh) & 0xffffu;
-        *reinterpret_cast<u32x2*>(vt + (8 * vc + e) * kVtPitch) =
-            u32x2{v0 | (v1 << 16), v2 | (v3 << 16)};
-      }
+    for (int wd = 0; wd < 4; ++wd) {  // dims 2 wd (low halves) and 2 wd + 1 (high)
+      *reinterpret_cast<u32x2*>(vt + (8 * vc + 2 * wd) * kVtPitch) =
+          u32x2{pack_lo(x[0][wd], x[1][wd]), pack_lo(x[2][wd], x[3][wd])};
+      *reinterpret_cast<u32x2*>(vt + (8 * vc + 2 * wd + 1) * kVtPitch) =
+          u32x2{pack_hi(x[0][wd], x[1][wd]), pack_hi(x[2][wd], x[3][wd])};
     }
   };
 
-  load_tile(0);
-  store_tile(0, lds);
-  __syncthreads();
+  // S^T of tile kt (K stage kt & 1); the two 32-key blocks alternate so that
+  // neighbouring MFMAs are independent
+  auto qk = [&](int kt, f32x16 (&s)[2]) {
+    const uint8_t* kp = lds + (kt & 1) * K_BYTES + col * KPITCH + 16 * hh;
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+        s[sb] = E::mfma(*reinterpret_cast<const u32x4*>(kp + 32 * sb * KPITCH + 32 * ks),
+                        qv[ks], s[sb]);
+  };
+  // -inf where a key is past the end or (causal) after the query; only the
+  // tiles that reach past the wave's first query or the end need it
+  auto mask = [&](int kt, f32x16 (&s)[2]) {
+    const int k0 = kt * kPfKTile;
+    if ((a.causal && k0 + kPfKTile - 1 > wq0) || k0 + kPfKTile > len) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kv = k0 + 32 * sb + 8 * (i >> 2) + 4 * hh + (i & 3);
+          const bool ok = kv < len && (!a.causal || kv <= qi);
+          s[sb][i] = ok ? s[sb][i] : -INFINITY;
+        }
+    }
+  };
 
   f32x16 o[DB];
 #pragma unroll
@@ -182,69 +233,76 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(Prefil
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
   float m = -INFINITY, lsum = 0.f;
-  const int wq_max = q0 + 32 * w + 31;
 
+  // softmax of a masked S^T tile and O^T += V^T . P^T (V stage kt & 1)
+  auto softmax_pv = [&](int kt, f32x16 (&s)[2]) {
+    float bm = -INFINITY;  // raw-score max (the scale is positive)
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2)
+        bm = __builtin_fmaxf(bm, __builtin_fmaxf(s[sb][i], s[sb][i + 1]));
+    bm = fmaxf(bm, __shfl_xor(bm, 32)) * a.scale_log2;
+    if (__builtin_amdgcn_ballot_w64(bm > m + kPfRescaleSlack)) {
+      const float mn = fmaxf(m, bm);
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 while m = -inf
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+      m = mn;
+    }
+    const float nms = m == -INFINITY ? 0.f : -m;
+    u32x4 pb[4];  // P^T operands of the four 16-key steps
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int sb = kk >> 1, base = 8 * (kk & 1);
+      uint32_t pw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p0 =
+            __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][base + 2 * j], a.scale_log2, nms));
+        const float p1 =
+            __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][base + 2 * j + 1], a.scale_log2, nms));
+        lsum += p0 + p1;
+        pw[j] = E::pack(p0, p1);
+      }
+      pb[kk] = u32x4{pw[0], pw[1], pw[2], pw[3]};
+    }
+    const uint8_t* vp = lds + 2 * K_BYTES + (kt & 1) * V_BYTES + col * kVtPitch + 16 * hh;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        o[db] = E::mfma(*reinterpret_cast<const u32x4*>(vp + 32 * db * kVtPitch + 32 * kk),
+                        pb[kk], o[db]);
+  };
+
+  // K and V of tile kt + 1 are loaded while tile kt is computed.  Two
+  // workgroups per CU overlap each other's softmax and matrix work; issuing
+  // the next tile's S^T before the softmax inside the wave (a one-tile
+  // pipeline) measured 1.8x slower, as its second S^T buffer leaves room for
+  // one workgroup per CU only.
+  load_k(0);
+  load_v(0);
+  store_k(0);
+  store_v(0, 0);
+  __syncthreads();
   for (int kt = 0; kt < n_kt; ++kt) {
     const bool more = kt + 1 < n_kt;
-    if (more) load_tile(kt + 1);
-    const uint8_t* kl = lds + (kt & 1) * STAGE;
-    const uint8_t* vl = kl + K_BYTES;
-    const int k0 = kt * kPfKTile;
-    if (!a.causal || k0 <= wq_max) {  // uniform over the wave
-      f32x16 s[2];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
-        const uint8_t* kp = kl + (32 * sb + col) * KPITCH + 16 * hh;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          s[sb] = E::mfma(*reinterpret_cast<const u32x4*>(kp + 32 * ks), qv[ks], s[sb]);
-      }
-      float x[2][16];
-      float bm = -INFINITY;
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kv = k0 + 32 * sb + 8 * (i >> 2) + 4 * hh + (i & 3);
-          const bool ok = kv < len && (!a.causal || kv <= qi);
-          x[sb][i] = ok ? s[sb][i] * a.scale_log2 : -INFINITY;
-          bm = fmaxf(bm, x[sb][i]);
-        }
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
-      if (__builtin_amdgcn_ballot_w64(bm > m + kPfRescaleSlack)) {
-        const float mn = fmaxf(m, bm);
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 while m = -inf
-        lsum *= alpha;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db] *= alpha;
-        m = mn;
-      }
-      const float ms = m == -INFINITY ? 0.f : m;
-      u32x4 pb[4];  // P^T operands of the four 16-key steps
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int sb = kk >> 1, base = 8 * (kk & 1);
-        uint32_t pw[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float p0 = __builtin_amdgcn_exp2f(x[sb][base + 2 * j] - ms);
-          const float p1 = __builtin_amdgcn_exp2f(x[sb][base + 2 * j + 1] - ms);
-          lsum += p0 + p1;
-          pw[j] = E::to16(p0) | (E::to16(p1) << 16);
-        }
-        pb[kk] = u32x4{pw[0], pw[1], pw[2], pw[3]};
-      }
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint8_t* vp = vl + (32 * db + col) * kVtPitch + 16 * hh;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-          o[db] = E::mfma(*reinterpret_cast<const u32x4*>(vp + 32 * kk), pb[kk], o[db]);
-      }
+    if (more) {
+      load_k(kt + 1);
+      load_v(kt + 1);
     }
-    if (more) store_tile(kt + 1, lds + ((kt + 1) & 1) * STAGE);
+    f32x16 sc[2];
+    if (!a.causal || kt * kPfKTile <= wq0 + 31) {
+      qk(kt, sc);
+      mask(kt, sc);
+      softmax_pv(kt, sc);
+    }
+    if (more) {
+      store_k((kt + 1) & 1);
+      store_v(kt + 1, (kt + 1) & 1);
+    }
     __syncthreads();
   }
 
@@ -258,10 +316,30 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(Prefil
       for (int g = 0; g < 4; ++g) {
         const f32x16& r = o[db];
         *reinterpret_cast<u32x2*>(op + (32 * db + 8 * g) * 2) =
-            u32x2{E::to16(r[4 * g] * inv) | (E::to16(r[4 * g + 1] * inv) << 16),
-                  E::to16(r[4 * g + 2] * inv) | (E::to16(r[4 * g + 3] * inv) << 16)};
+            u32x2{E::pack(r[4 * g] * inv, r[4 * g + 1] * inv),
+                  E::pack(r[4 * g + 2] * inv, r[4 * g + 3] * inv)};
       }
   }
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(PrefillArgs a) {
+  constexpr int K_BYTES = kPfKTile * (D * 2 + 16);
+  constexpr int V_BYTES = D * kVtPitch;
+  // two K stages, then two V^T stages
+  __shared__ __align__(16) uint8_t lds[2 * K_BYTES + 2 * V_BYTES];
+  const int hb = a.n_q_heads * a.batch;
+  const int job = blockIdx.x;
+  const int tile = a.n_qtiles - 1 - job / hb;
+  const int h = (job % hb) / a.batch;
+  const int b = job % a.batch;
+  int64_t s0 = a.cu_seqlens[b], s1 = a.cu_seqlens[b + 1];
+  s0 = min(max(s0, (int64_t)0), a.total_tokens);
+  s1 = min(max(s1, s0), a.total_tokens);
+  const int len = (int)min(s1 - s0, (int64_t)a.max_seqlen);
+  const int q0 = tile * kPfQTile;
+  if (q0 >= len) return;  // uniform over the workgroup, before any barrier
+  attend_tile<DT, D>(a, lds, h, s0, len, q0);
 }
 
 template <int DT, int D>
@@ -302,8 +380,9 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
       q_token_stride % 8 || k_token_stride % 8 || v_token_stride % 8 || out_token_stride % 8)
     return AEGKV_ERR_MISALIGNED;
   const int64_t n_qtiles = ((int64_t)max_seqlen + kPfQTile - 1) / kPfQTile;
-  const int64_t grid = n_qtiles * n_q_heads * batch;
-  if (grid > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
+  const int64_t n_jobs = n_qtiles * n_q_heads * batch;
+  if (n_jobs > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
+  const int64_t grid = n_jobs;
 
   PrefillArgs a;
   a.q = static_cast<const uint8_t*>(q);
