@@ -27,7 +27,8 @@ attention (Qwen2.5-7B GQA 28/4, 128 sequences, lognormal mean 1500, up to 8192
 tokens) in us per layer; block pack and scatter for the Llama-2-13B swap
 workload (32 x 2048 tokens, 4096 blocks of 12.5 MiB) plus a sampled PCIe leg to
 pinned host; defrag of the unified multi-model pool followed by a Yi-1.5-9B
-decode step (append + attention); token gather; device-side input preparation
+decode step (append + attention); token gather; the prefill side (prompt KV
+write and causal varlen attention, 4 x 2048 tokens); device-side input preparation
 against the reference's host loops; the block manager's host bookkeeping
 (native against the reference's algorithm, same block ids).
 
@@ -52,6 +53,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
 METRIC = "KV gather/append GB/s (%HBM peak); paged decode-attn µs/layer @Qwen2.5-7B"
 ROTATE_STEPS = 32
 
@@ -407,6 +409,68 @@ def bench_prepare(args, timer):
     return out
 
 
+# ------------------------------------------------------------------------- prefill
+PREFILL_LENS = [2048] * 4   # the reference's profiled prefill shape i2048b4
+
+
+def bench_prefill(args, timer):
+    """Prompt run of a Qwen2.5-7B prefill engine, 4 prompts x 2048 tokens:
+    per layer, the KV write of every prompt token (reshape_and_cache_flash
+    with the prompt's slot mapping) and causal varlen attention
+    (flash_attn_varlen_func), GQA 28/4, D 128, bf16.  q/k/v are views of one
+    fused [tokens, (28 + 8) * 128] projection output per layer, 28 layers of
+    distinct inputs, so the append reads HBM, not cache.  Causal FLOPs:
+    2 * Hq * D * n * (n + 1) per sequence (QK and PV)."""
+    import torch
+    from aegaeon_amd import attention as A
+    from aegaeon_amd.workloads import QWEN25_7B, split_tables
+    dev = torch.device("cuda", 0)
+    g = QWEN25_7B
+    L, Hq, Hkv, D = g.n_layers, g.n_q_heads, g.n_kv_heads, g.head_dim
+    lens = PREFILL_LENS
+    T = sum(lens)
+    rng = np.random.default_rng(args.seed)
+    need = [-(-n // g.block_size) for n in lens]
+    pool = 2 * sum(need)
+    tables = split_tables(rng.permutation(pool)[:sum(need)], need)
+    bs = g.block_size
+    # every prompt position p: table[p // 16] * 16 + p % 16 (worker.py:628-633)
+    slots = torch.from_numpy(np.concatenate(
+        [np.asarray(t, dtype=np.int64)[np.arange(n) // bs] * bs + np.arange(n) % bs
+         for t, n in zip(tables, lens)])).to(dev)
+    cache = torch.empty((pool, *g.block_shape), dtype=torch.bfloat16, device=dev)
+    view = cache.permute(1, 2, 0, 3, 4, 5)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 2)
+    qkv = torch.randn((L, T, (Hq + 2 * Hkv) * D), generator=gen, device=dev).to(torch.bfloat16)
+    q = qkv[..., :Hq * D].view(L, T, Hq, D)
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].view(L, T, Hkv, D)
+    v = qkv[..., (Hq + Hkv) * D:].view(L, T, Hkv, D)
+    out = torch.empty((T, Hq, D), dtype=torch.bfloat16, device=dev)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def append(i):
+        layer = i % L
+        A.reshape_and_cache_flash(k[layer], v[layer], view[layer, 0], view[layer, 1], slots)
+
+    def attend(i):
+        layer = i % L
+        A.flash_attn_varlen_func(q[layer], k[layer], v[layer], cu, cu, max(lens), max(lens),
+                                 softmax_scale=scale, causal=True, out=out)
+
+    for i in range(L):
+        append(i)
+        attend(i)
+    torch.cuda.synchronize()
+    app_ms, _ = timer.run(append, 4 * L)
+    att_ms, _ = timer.run(attend, 2 * L)
+    flops = sum(2 * Hq * D * n * (n + 1) for n in lens)
+    app_bytes = 2 * T * 2 * Hkv * D * 2 + 8 * T
+    del cache, qkv
+    torch.cuda.empty_cache()
+    return {"append_ms": app_ms, "append_bytes": app_bytes, "attn_ms": att_ms, "flops": flops}
+
+
 # ------------------------------------------------------------------- block manager
 BM_POOL_BLOCKS = 200_000           # 175 GiB of 0.875 MiB Qwen2.5-7B blocks on one GPU
 BM_CPU_SLABS, BM_SLAB_BYTES = 128, 1 << 30   # aegaeon/aegaeon/config.py:37-39
@@ -554,8 +618,8 @@ def main(argv=None):
     p.add_argument("--swap-seqs", type=int, default=32)
     p.add_argument("--pcie-blocks", type=int, default=64)
     p.add_argument("--only", default="all",
-                   help="comma list of append,attention,pack,defrag,gather,prepare,bm,calib "
-                        "or 'all'")
+                   help="comma list of append,attention,pack,defrag,gather,prefill,prepare,bm,"
+                        "calib or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU and "
@@ -570,13 +634,14 @@ def main(argv=None):
     torch.cuda.set_device(0)
     log(f"device: {torch.cuda.get_device_name(0)}")
     only = set(args.only.split(",")) if args.only != "all" else \
-        {"append", "attention", "pack", "defrag", "gather", "prepare", "bm", "calib"}
+        {"append", "attention", "pack", "defrag", "gather", "prefill", "prepare", "bm", "calib"}
     timer = Timer()
     log(f"spin calibration: {timer.cycles_per_ms:.0f} cycles/ms")
     res = {}
     for name, fn in (("append", bench_append), ("attention", bench_attention),
                      ("gather", bench_gather), ("pack", bench_pack), ("defrag", bench_defrag),
-                     ("prepare", bench_prepare), ("bm", bench_block_manager),
+                     ("prefill", bench_prefill), ("prepare", bench_prepare),
+                     ("bm", bench_block_manager),
                      ("calib", bench_calib)):
         if name in only:
             t0 = time.perf_counter()
@@ -657,6 +722,19 @@ def main(argv=None):
         ops_out["prepare_inputs_us_per_step"] = {
             k: {"device": round(v["device"], 1), "reference_host_loops": round(v["reference_host"], 1)}
             for k, v in res["prepare"].items()}
+    if "prefill" in res:
+        pf = res["prefill"]
+        tf = pf["flops"] / (pf["attn_ms"] * 1e-3) / 1e12
+        ag = pf["append_bytes"] / (pf["append_ms"] * 1e-3) / 1e9
+        ops_out["prefill_qwen_4x2048"] = {
+            "workload": "Qwen2.5-7B prompt run, 4 prompts x 2048 tokens (profiled shape i2048b4), "
+                        "GQA 28/4, D 128, bf16, 28 layers of distinct q/k/v views of a fused QKV",
+            "attention_us_per_layer": round(pf["attn_ms"] * 1e3, 2),
+            "attention_flops_per_layer": pf["flops"], "TFLOP/s": round(tf, 1),
+            "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "kv_write_us_per_layer": round(pf["append_ms"] * 1e3, 2),
+            "kv_write_bytes_per_layer": pf["append_bytes"], "kv_write_GB/s": round(ag, 1),
+            "kv_write_frac_hbm": round(ag / HBM_PEAK_GBS, 4)}
     if "bm" in res:
         b = res["bm"]
         ops_out["block_manager"] = {
