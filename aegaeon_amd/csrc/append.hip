@@ -82,6 +82,19 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(AppendArgs a)
 // One workgroup per (logical block, sequence, layer*2+kv): the tokens of a
 // block are contiguous rows in both the cache and the output, so the work is a
 // straight copy of n_tok * row bytes.
+// gather_tokens: a tile is one logical block (<= block_size tokens) of one
+// sequence for one (layer, K/V).  Each workgroup scans the batch's tile counts
+// into LDS, then a persistent grid walks the flattened (layer, K/V, sequence,
+// block) tiles round-robin; the block id and output row of a workgroup's next
+// tile are fetched while the current tile's non-temporal loads are in flight.
+// (One workgroup per tile spent a dependent id load per 16 KiB and ran at
+// 4.9 TB/s on the Qwen2.5-7B batch; this walk reaches 5.3-5.4 TB/s, about 86%
+// of a plain contiguous non-temporal copy on the same GPU.)
+constexpr int kGatherThreads = 256;
+constexpr int kGatherMaxBatch = 1024;  // sequences per launch (LDS scan)
+constexpr int kGatherWorkgroupsPerCu = 32;  // 4..32 measured within 3% (32 best)
+constexpr uint32_t kGatherPassBytes = kGatherThreads * 16 * 4;  // 16 KiB per pass
+
 struct GatherArgs {
   const uint8_t* kc;
   const uint8_t* vc;
@@ -98,30 +111,121 @@ struct GatherArgs {
   int64_t out_layer_b;
   uint32_t row_bytes;
   uint32_t block_size;
+  int32_t batch;       // <= kGatherMaxBatch
+  int32_t n_lk;        // 2 * n_layers
 };
 
-__global__ __launch_bounds__(256) void gather_tokens_kernel(GatherArgs a) {
-  const int i = blockIdx.x, b = blockIdx.y;
-  const int layer = blockIdx.z >> 1, kv = blockIdx.z & 1;
-  const int len = min(max(a.seq_lens[b], 0), a.max_seq_len);
-  const int first = i * (int)a.block_size;
-  if (first >= len) return;
-  const int64_t row0 = (int64_t)a.cu_seqlens[b] + first;  // first output token
-  if (row0 < 0 || row0 >= a.out_tokens) return;
-  const int n_tok = (int)min((int64_t)min((int)a.block_size, len - first), a.out_tokens - row0);
-  const int32_t id = a.block_tables[(int64_t)b * a.max_blocks + i];
-  if (id < 0 || id >= a.n_blocks) return;
-  const uint8_t* src = (kv ? a.vc : a.kc) + layer * a.layer_b + (int64_t)id * a.blk_b;
-  uint8_t* dst = (kv ? a.out_v : a.out_k) + layer * a.out_layer_b + row0 * a.row_bytes;
-  const uint32_t n_chunks = (uint32_t)n_tok * (a.row_bytes / 16);
-  for (uint32_t c = threadIdx.x; c < n_chunks; c += 4 * 256) {
+__global__ __launch_bounds__(kGatherThreads) void gather_tokens_kernel(GatherArgs a) {
+  __shared__ int32_t pre[kGatherMaxBatch + 1];  // first tile of each sequence
+  __shared__ int32_t lens[kGatherMaxBatch];
+  __shared__ int32_t wsum[kGatherThreads / 64];
+  constexpr int PER = kGatherMaxBatch / kGatherThreads;
+  const int t = threadIdx.x, B = a.batch;
+  const int bs = (int)a.block_size;
+  int cnt[PER], run = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {  // loads issued together, clamped in bounds
+    const int b = t * PER + k;
+    const int raw = a.seq_lens[min(b, B - 1)];
+    const int len = b < B ? min(max(raw, 0), a.max_seq_len) : 0;
+    if (b < B) lens[b] = len;
+    cnt[k] = (len + bs - 1) / bs;
+    run += cnt[k];
+  }
+  int incl = run;  // inclusive scan over the workgroup
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if ((t & 63) >= off) incl += y;
+  }
+  if ((t & 63) == 63) wsum[t >> 6] = incl;
+  __syncthreads();
+  int excl = incl - run;
+  for (int w = 0; w < (t >> 6); ++w) excl += wsum[w];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int b = t * PER + k;
+    if (b <= B) pre[b] = excl;
+    excl += cnt[k];
+  }
+  if (t == kGatherThreads - 1) pre[B] = excl;  // total (B may equal the capacity)
+  __syncthreads();
+  const int64_t T = pre[B];
+  const int64_t total = T * a.n_lk;
+  int64_t g = blockIdx.x;
+  if (g >= total) return;  // uniform
+
+  // tile g -> (lk, b, j): b is the last sequence whose first tile is <= r
+  auto locate = [&](int64_t gg, int& lk, int& b, int& j) {
+    lk = (int)(gg / T);
+    const int r = (int)(gg - (int64_t)lk * T);
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre[mid] <= r) lo = mid;
+      else hi = mid - 1;
+    }
+    b = lo;
+    j = r - pre[lo];
+  };
+  int lk, b, j;
+  locate(g, lk, b, j);
+  int32_t id = a.block_tables[(int64_t)b * a.max_blocks + j];
+  int64_t row0 = a.cu_seqlens[b];
+  while (true) {
+    // current tile
+    const int layer = lk >> 1, kv = lk & 1;
+    const int64_t row = row0 + (int64_t)j * bs;
+    int n_tok = min(bs, lens[b] - j * bs);
+    if (row < 0 || row >= a.out_tokens || id < 0 || id >= a.n_blocks) n_tok = 0;
+    else n_tok = (int)min((int64_t)n_tok, a.out_tokens - row);
+    const uint32_t bytes = (uint32_t)n_tok * a.row_bytes;
+    const u32x4* sp = reinterpret_cast<const u32x4*>(
+        (kv ? a.vc : a.kc) + layer * a.layer_b + (int64_t)max(id, 0) * a.blk_b);
+    u32x4* dp = reinterpret_cast<u32x4*>((kv ? a.out_v : a.out_k) + layer * a.out_layer_b +
+                                         max(row, (int64_t)0) * a.row_bytes);
     u32x4 r[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (c + k * 256 < n_chunks) r[k] = reinterpret_cast<const u32x4*>(src)[c + k * 256];
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t c = k * kGatherThreads + t;
+      if (c * 16 < bytes) r[k] = __builtin_nontemporal_load(sp + c);
+    }
+    // next tile's id and output row, in flight with the loads above
+    const int64_t gn = g + gridDim.x;
+    const bool more = gn < total;
+    int nlk = lk, nb = b, nj = j;
+    int32_t nid = id;
+    int64_t nrow0 = row0;
+    if (more) {
+      locate(gn, nlk, nb, nj);
+      nid = a.block_tables[(int64_t)nb * a.max_blocks + nj];
+      nrow0 = a.cu_seqlens[nb];
+    }
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (c + k * 256 < n_chunks) reinterpret_cast<u32x4*>(dst)[c + k * 256] = r[k];
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t c = k * kGatherThreads + t;
+      if (c * 16 < bytes) __builtin_nontemporal_store(r[k], dp + c);
+    }
+    // rows wider than 1 KiB: the rest of the tile, 16 KiB per pass
+    for (uint32_t base = kGatherPassBytes / 16; base * 16 < bytes; base += kGatherPassBytes / 16) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t c = base + k * kGatherThreads + t;
+        if (c * 16 < bytes) r[k] = __builtin_nontemporal_load(sp + c);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t c = base + k * kGatherThreads + t;
+        if (c * 16 < bytes) __builtin_nontemporal_store(r[k], dp + c);
+      }
+    }
+    if (!more) break;
+    g = gn;
+    lk = nlk;
+    b = nb;
+    j = nj;
+    id = nid;
+    row0 = nrow0;
   }
 }
 
@@ -206,17 +310,18 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
     return AEGKV_ERR_MISALIGNED;
   const int64_t blocks_needed = ((int64_t)max_seq_len + block_size - 1) / block_size;
   if (blocks_needed > max_blocks) return AEGKV_ERR_INVALID_ARG;
-  if (batch > 65535 || (int64_t)n_layers * 2 > 65535) return AEGKV_ERR_UNSUPPORTED;
+  if (blocks_needed * kGatherMaxBatch > INT32_MAX || (int64_t)n_layers * 2 > 65535)
+    return AEGKV_ERR_UNSUPPORTED;
+  DeviceState* ds = nullptr;
+  int rc = current_device_state(&ds);
+  if (rc) return rc;
   GatherArgs a;
   a.kc = static_cast<const uint8_t*>(key_cache);
   a.vc = static_cast<const uint8_t*>(value_cache);
   a.blk_b = cache_block_stride * e;
   a.layer_b = cache_layer_stride * e;
   a.n_blocks = n_blocks;
-  a.block_tables = block_tables;
   a.max_blocks = max_blocks;
-  a.seq_lens = seq_lens;
-  a.cu_seqlens = cu_seqlens;
   a.out_k = static_cast<uint8_t*>(out_key);
   a.out_v = static_cast<uint8_t*>(out_value);
   a.out_tokens = out_tokens;
@@ -224,9 +329,20 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
   a.out_layer_b = out_layer_stride * e;
   a.row_bytes = (uint32_t)row_bytes;
   a.block_size = (uint32_t)block_size;
-  hipLaunchKernelGGL(gather_tokens_kernel, dim3((uint32_t)blocks_needed, batch, n_layers * 2),
-                     dim3(256), 0, (hipStream_t)stream, a);
-  AEGKV_HIP_TRY(hipGetLastError());
+  a.n_lk = 2 * n_layers;
+  const int64_t max_grid = (int64_t)std::max(ds->num_cu, 1) * kGatherWorkgroupsPerCu;
+  for (int32_t b0 = 0; b0 < batch; b0 += kGatherMaxBatch) {
+    const int32_t nb = std::min(kGatherMaxBatch, batch - b0);
+    a.batch = nb;
+    a.block_tables = block_tables + (int64_t)b0 * max_blocks;
+    a.seq_lens = seq_lens + b0;
+    a.cu_seqlens = cu_seqlens + b0;
+    const int64_t tiles_max = blocks_needed * nb * a.n_lk;  // upper bound of the tiles
+    const uint32_t grid = (uint32_t)std::max<int64_t>(1, std::min(tiles_max, max_grid));
+    hipLaunchKernelGGL(gather_tokens_kernel, dim3(grid), dim3(kGatherThreads), 0,
+                       (hipStream_t)stream, a);
+    AEGKV_HIP_TRY(hipGetLastError());
+  }
   return AEGKV_OK;
 }
 

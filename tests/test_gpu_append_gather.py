@@ -119,3 +119,84 @@ def test_gather_qwen_layers_subset(device):
     rk, rv = ko.gather_tokens(bits, tables, lens, layers=[5, 6, 7])
     assert np.array_equal(to_bits(out_k), rk)
     assert np.array_equal(to_bits(out_v), rv)
+
+
+def _tables_for(rng, lens, N):
+    need = [-(-int(x) // 16) for x in lens]
+    assert sum(need) <= N
+    ids = rng.permutation(N)[:sum(need)]
+    tables, o = [], 0
+    for c in need:
+        tables.append([int(x) for x in ids[o:o + c]])
+        o += c
+    return tables
+
+
+def test_gather_batch_above_one_launch(device):
+    """2500 sequences (lengths 0..40) run as three launches of <= 1024."""
+    rng = np.random.default_rng(31)
+    N, L, H, D = 6000, 2, 2, 64                         # about 4500 blocks needed
+    bits = random_bits(rng, (N, L, 2, 16, H, D), "fp16")
+    cache = to_device_bits(bits, "fp16", device)
+    lens = rng.integers(0, 41, 2500).astype(np.int64)
+    tables = _tables_for(rng, lens, N)
+    bt = torch.from_numpy(ko.pad_block_tables(tables)).to(device)
+    out_k, out_v = A.gather_tokens(cache, bt, torch.from_numpy(lens.astype(np.int32)).to(device),
+                                   int(lens.sum()), int(lens.max()))
+    rk, rv = ko.gather_tokens(bits, tables, lens)
+    assert np.array_equal(to_bits(out_k), rk)
+    assert np.array_equal(to_bits(out_v), rv)
+
+
+def test_gather_wide_rows(device):
+    """Llama-2-13B rows (40 heads x 128 = 10 KiB): a 16-token block is 160 KiB,
+    copied in several 16 KiB passes."""
+    rng = np.random.default_rng(32)
+    N, L, H, D = 24, 1, 40, 128
+    bits = random_bits(rng, (N, L, 2, 16, H, D), "fp16")
+    cache = to_device_bits(bits, "fp16", device)
+    lens = np.asarray([16, 1, 37, 0, 95], dtype=np.int64)
+    tables = _tables_for(rng, lens, N)
+    bt = torch.from_numpy(ko.pad_block_tables(tables)).to(device)
+    out_k, out_v = A.gather_tokens(cache, bt, torch.from_numpy(lens.astype(np.int32)).to(device),
+                                   int(lens.sum()), int(lens.max()))
+    rk, rv = ko.gather_tokens(bits, tables, lens)
+    assert np.array_equal(to_bits(out_k), rk)
+    assert np.array_equal(to_bits(out_v), rv)
+
+
+def test_gather_clips_capacity_bad_ids_and_long_lengths(device):
+    """Output rows past the capacity, blocks with ids outside the pool and
+    tokens past the host bound max_seq_len are never written."""
+    rng = np.random.default_rng(33)
+    N, L, H, D = 40, 1, 2, 64
+    bits = random_bits(rng, (N, L, 2, 16, H, D), "bf16")
+    cache = to_device_bits(bits, "bf16", device)
+    lens = np.asarray([20, 33, 50], dtype=np.int64)
+    tables = _tables_for(rng, lens, N)
+    tables[1][1] = N + 7                                # tokens 16..31 of sequence 1
+    bt = torch.from_numpy(ko.pad_block_tables(tables)).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    max_len, cap = 40, 80                               # sequence 2 clamped to 40 tokens
+    cu = torch.tensor([0, 20, 53, 93], dtype=torch.int32, device=device)
+    es = cache.element_size()
+    ok = torch.full((1, cap, H, D), 7.0, dtype=cache.dtype, device=device)
+    ov = torch.full_like(ok, 7.0)
+    from aegaeon_amd import _lib
+    base = cache.data_ptr()
+    rc = _lib.load().aegkv_gather_tokens(
+        base, base + 16 * H * D * es, cache.stride(0), cache.stride(1), N, bt.data_ptr(),
+        bt.size(1), sl.data_ptr(), cu.data_ptr(), 3, max_len, ok.data_ptr(), ov.data_ptr(), cap,
+        cap * H * D, 1, 16, H, D, es, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    good = [t if i != 1 else [t[0], 0, t[2]] for i, t in enumerate(tables)]
+    rk, rv = ko.gather_tokens(bits, good, [20, 33, 40])
+    sentinel = to_bits(torch.full((1,), 7.0, dtype=cache.dtype))[0]
+    gk, gv = to_bits(ok)[0], to_bits(ov)[0]
+    want_rows = list(range(0, 20)) + list(range(20, 36)) + list(range(52, 53)) + \
+        list(range(53, 80))                             # seq 2 rows 53..92 clipped at 80
+    src_rows = list(range(0, 20)) + list(range(20, 36)) + list(range(52, 53)) + \
+        list(range(53, 80))
+    for out, ref in ((gk, rk[0]), (gv, rv[0])):
+        assert np.array_equal(out[want_rows], ref[src_rows])
+        assert (out[36:52] == sentinel).all()           # the bad block's 16 tokens
