@@ -46,15 +46,12 @@ def prepare_model_inputs(requests: Sequence[Tuple], block_tables: Sequence[Seque
         raise ValueError("empty batch")  # the reference asserts (worker.py:594)
     if len(block_tables) != len(requests):
         raise ValueError("one block table per request")
-    device = torch.device(device)
     B = len(requests)
     # one C-speed pass over each list (the lists are the block manager's)
     seq = np.fromiter((r[2] for r in requests), dtype=np.int32, count=B)
     ctx = np.fromiter((r[3] for r in requests), dtype=np.int32, count=B)
-    qlen = seq.astype(np.int64) - ctx
-    is_prompt = ctx == 0
     ntok = np.fromiter((len(r[1]) for r in requests), dtype=np.int64, count=B)
-    if not np.array_equal(ntok, qlen):
+    if not np.array_equal(ntok, seq.astype(np.int64) - ctx):
         raise ValueError("a request's tokens must be its seq_len - context_len new tokens")
     lens = np.fromiter(map(len, block_tables), dtype=np.int64, count=B)
     offsets = np.zeros(B + 1, dtype=np.int64)
@@ -62,10 +59,38 @@ def prepare_model_inputs(requests: Sequence[Tuple], block_tables: Sequence[Seque
     ids = np.fromiter(itertools.chain.from_iterable(block_tables), dtype=np.int32,
                       count=int(offsets[-1]))
     tokens = np.fromiter(itertools.chain.from_iterable(r[1] for r in requests), dtype=np.int64,
-                         count=int(qlen.sum()))
+                         count=int(ntok.sum()))
+    return prepare_inputs_from_arrays(ids, offsets, seq, ctx, tokens, device, block_size)
+
+
+def prepare_inputs_from_arrays(table_ids: np.ndarray, table_offsets: np.ndarray,
+                               seq_lens: np.ndarray, context_lens: np.ndarray,
+                               tokens: np.ndarray, device, block_size: int = BLOCK_SIZE
+                               ) -> Tuple[torch.Tensor, torch.Tensor, Dict]:
+    """The same outputs as :func:`prepare_model_inputs`, from arrays: request
+    b's block table is ``table_ids[table_offsets[b]:table_offsets[b + 1]]``
+    (int32; the layout ``BlockManager.flat_block_tables`` returns), its
+    lengths ``seq_lens[b]`` / ``context_lens[b]`` (int32) and its new tokens
+    the next ``seq_len - context_len`` entries of ``tokens`` (int64)."""
+    device = torch.device(device)
+    ids = np.ascontiguousarray(table_ids, dtype=np.int32)
+    offsets = np.ascontiguousarray(table_offsets, dtype=np.int64)
+    seq = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    ctx = np.ascontiguousarray(context_lens, dtype=np.int32)
+    tokens = np.ascontiguousarray(tokens, dtype=np.int64)
+    B = seq.size
+    if B == 0:
+        raise ValueError("empty batch")  # the reference asserts (worker.py:594)
+    if ctx.size != B or offsets.size != B + 1:
+        raise ValueError("one context length and one table per request")
+    qlen = seq.astype(np.int64) - ctx
+    is_prompt = ctx == 0
+    lens = np.diff(offsets)
     # decode rows keep their table, prefill rows are empty (worker.py:600-605)
     pad_width = int(lens[~is_prompt].max()) if (~is_prompt).any() else 0
     T = int(qlen.sum())
+    if tokens.size != T:
+        raise ValueError("tokens must hold every request's new tokens")
 
     i32 = dict(dtype=torch.int32, device=device)
     i64 = dict(dtype=torch.int64, device=device)
@@ -92,7 +117,7 @@ def prepare_model_inputs(requests: Sequence[Tuple], block_tables: Sequence[Seque
         slot_mapping=slots,
         num_prefill_tokens=int(qlen[is_prompt].sum()),
         num_decode_tokens=int(qlen[~is_prompt].sum()),
-        seq_lens=[int(x) for x in seq],
+        seq_lens=seq.tolist(),
         seq_lens_tensor=seq_t,
         max_query_len=int(qlen.max()),
         max_prefill_seq_len=int(prefill_lens.max()) if prefill_lens.size else 0,

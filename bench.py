@@ -368,10 +368,11 @@ def bench_gather(args, timer):
 def bench_prepare(args, timer):
     """Per-step metadata (slot mapping, padded tables, lengths, start offsets)
     for the Qwen2.5-7B decode batch (256 requests) and a prefill batch (8
-    prompts of 2048 tokens): the library's one upload + one kernel against the
-    reference's host loops (the oracle's restatement of worker.py:596-676)
-    followed by the reference's eight host-to-device tensors.  Wall time per
-    step, synchronised, host work included."""
+    prompts of 2048 tokens): the library's one upload + one kernel, fed from the
+    reference's request lists or from arrays (the block manager's flat tables),
+    against the reference's host loops (the oracle's restatement of
+    worker.py:596-676) followed by the reference's eight host-to-device
+    tensors.  Wall time per step, synchronised, host work included."""
     import torch
     from aegaeon_amd import inputs as I
     from aegaeon_amd.workloads import qwen_append_batch
@@ -394,7 +395,15 @@ def bench_prepare(args, timer):
 
     for name, (reqs, tables) in cases.items():
         times = {}
+        # the same batch as arrays (the block manager's flat_block_tables layout)
+        offs = np.concatenate([[0], np.cumsum([len(t) for t in tables])]).astype(np.int64)
+        ids = np.concatenate([np.asarray(t, dtype=np.int32) for t in tables])
+        seq = np.asarray([r[2] for r in reqs], dtype=np.int32)
+        ctx = np.asarray([r[3] for r in reqs], dtype=np.int32)
+        toks = np.concatenate([np.asarray(r[1], dtype=np.int64) for r in reqs])
         for label, fn in (("device", lambda: I.prepare_model_inputs(reqs, tables, dev)),
+                          ("device_from_arrays",
+                           lambda: I.prepare_inputs_from_arrays(ids, offs, seq, ctx, toks, dev)),
                           ("reference_host", lambda: reference_path(reqs, tables))):
             for _ in range(3):
                 fn()
@@ -720,7 +729,9 @@ def main(argv=None):
             "yi_attention_GB/s": round(tg, 1), "yi_attention_frac_hbm": round(tg / HBM_PEAK_GBS, 4)}
     if "prepare" in res:
         ops_out["prepare_inputs_us_per_step"] = {
-            k: {"device": round(v["device"], 1), "reference_host_loops": round(v["reference_host"], 1)}
+            k: {"device_from_request_lists": round(v["device"], 1),
+                "device_from_arrays": round(v["device_from_arrays"], 1),
+                "reference_host_loops": round(v["reference_host"], 1)}
             for k, v in res["prepare"].items()}
     if "prefill" in res:
         pf = res["prefill"]

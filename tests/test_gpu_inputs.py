@@ -74,3 +74,24 @@ def test_qwen_decode_batch(device):
 def test_short_table_raises(device):
     with pytest.raises(AegkvError):
         I.prepare_model_inputs([(0, [1], 17, 16)], [[3]], device)
+
+
+def test_arrays_from_block_manager(device):
+    """Block tables straight from the native block manager's flat layout give
+    the same outputs as the list path and the oracle."""
+    from aegaeon_amd.block_manager import BlockManager
+    rng = np.random.default_rng(17)
+    bm = BlockManager(0, 1)
+    bm.register_gpu_space(0, 4096, (28, 2, 16, 4, 128))
+    ctx = rng.integers(1, 900, 40)
+    rids = list(range(40))
+    bm.allocate_blocks_by_count(rids, [int(-(-(c + 1) // 16)) for c in ctx], 0)
+    for r in rids[::3]:                                  # scatter the free list
+        bm.free_blocks(r)
+    bm.allocate_blocks_by_count(rids[::3], [int(-(-(ctx[r] + 1) // 16)) for r in rids[::3]], 0)
+    offsets, ids = bm.flat_block_tables(rids)
+    reqs = I.decode_requests(ctx)
+    tokens = np.asarray([r[1][0] for r in reqs], dtype=np.int64)
+    got = I.prepare_inputs_from_arrays(ids, offsets, ctx + 1, ctx, tokens, device)
+    tables = [bm.get_block_table(r).blocks for r in rids]
+    _compare(got, ko.prepare_model_inputs(reqs, tables))
