@@ -15,11 +15,14 @@
 // units, sum).  A workgroup's range can end at most one cut sequence (a cut
 // sequence ending inside a range began before it, i.e. at the range's start),
 // so each workgroup leaves a 16-byte descriptor of that sequence (or none),
-// and a second kernel of one workgroup per descriptor merges its pieces with
-// log-sum-exp weights.  (Merging in the main kernel by the last piece to
-// arrive needs device-scope release fences, which write back the XCD's L2 and
-// measured 2x slower end to end.)  A sequence held by one workgroup is normalised
-// and written directly.
+// and a second kernel, one workgroup per descriptor and kv head, merges its
+// pieces with log-sum-exp weights.  A sequence held by one workgroup is
+// normalised and written directly.  (Merging in the main kernel by the last
+// piece to arrive measured slower both ways it was built: with device-scope
+// release fences, which write back the XCD's L2, 2x; with write-through
+// agent-scope partials and an epoch-tagged arrival counter, 13% on a ragged
+// batch, as every cut piece waits for its stores and the counter and the last
+// arrival merges a long sequence's pieces serially.)
 //
 // Inside a workgroup, wave w handles kv head grp * 4 + w, and all
 // G = Hq / Hkv query heads of that kv head are processed together, so each K/V
