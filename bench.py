@@ -27,7 +27,8 @@ attention (Qwen2.5-7B GQA 28/4, 128 sequences, lognormal mean 1500, up to 8192
 tokens) in us per layer; block pack and scatter for the Llama-2-13B swap
 workload (32 x 2048 tokens, 4096 blocks of 12.5 MiB) plus a sampled PCIe leg to
 pinned host; defrag of the unified multi-model pool followed by a Yi-1.5-9B
-decode step (append + attention); token gather; the prefill side (prompt KV
+decode step (append + attention); token gather; a swap-out on a side stream
+overlapped with 28 layers of decode attention; the prefill side (prompt KV
 write and causal varlen attention, 4 x 2048 tokens); device-side input preparation
 against the reference's host loops; the block manager's host bookkeeping
 (native against the reference's algorithm, same block ids).
@@ -418,6 +419,84 @@ def bench_prepare(args, timer):
     return out
 
 
+# ------------------------------------------------------------------------- overlap
+OVERLAP_SWAP_BLOCKS = 128   # 112 MiB of Qwen2.5-7B blocks
+
+
+def bench_overlap(args, timer):
+    """Swap-out on a side stream overlapped with compute: 28 layers of the
+    Qwen2.5-7B decode attention (128 sequences) on the compute stream while
+    128 scattered Qwen2.5-7B blocks (112 MiB) are swapped out to pinned host
+    memory on a second stream, as the reference's worker does with its swap
+    streams (worker.py:716-770).  Both streams are held behind a spin until
+    the host has enqueued everything; events give each stream's span."""
+    import torch
+    from aegaeon_amd import attention as A, ops
+    from aegaeon_amd.workloads import qwen_attention_batch
+    dev = torch.device("cuda", 0)
+    wb = qwen_attention_batch(args.seed)
+    g = wb.geometry
+    cache = torch.empty((wb.n_pool_blocks, *g.block_shape), dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 3)
+    _fill_random(cache, gen)
+    view = cache.permute(1, 2, 0, 3, 4, 5)
+    q = torch.randn((g.n_layers, wb.batch, g.n_q_heads, g.head_dim), generator=gen,
+                    device=dev).to(torch.bfloat16)
+    outs = torch.empty_like(q)
+    bt = torch.from_numpy(wb.padded_tables()).to(dev)
+    sl = torch.from_numpy(wb.seq_lens.astype(np.int32)).to(dev)
+    max_len = int(wb.seq_lens.max())
+    scale = 1.0 / math.sqrt(g.head_dim)
+    ws = A.attention_workspace(wb.batch, g.n_q_heads, g.n_kv_heads, g.head_dim, max_len,
+                               torch.bfloat16, 0, device=dev)
+    rng = np.random.default_rng(args.seed + 3)
+    src = rng.choice(wb.n_pool_blocks, OVERLAP_SWAP_BLOCKS, replace=False).astype(np.int64)
+    dst = np.arange(OVERLAP_SWAP_BLOCKS, dtype=np.int64)
+    host = torch.empty((OVERLAP_SWAP_BLOCKS, *g.block_shape), dtype=torch.bfloat16,
+                       pin_memory=True)
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(device=dev)
+
+    def attn_all():
+        for layer in range(g.n_layers):
+            A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], bt, sl, scale,
+                                     max_len, out=outs[layer], workspace=ws)
+
+    def swap_out():
+        with torch.cuda.stream(side):
+            ops.swap(src, dst, False, cache, host)
+
+    def span(run_attn: bool, run_swap: bool) -> float:
+        ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(20.0 * timer.cycles_per_ms))  # hold both streams
+        gate, e0, e_side, e_end = ev(), ev(), ev(), ev()
+        gate.record(main)
+        side.wait_event(gate)
+        e0.record(main)
+        if run_swap:
+            swap_out()
+        e_side.record(side)
+        if run_attn:
+            attn_all()
+        main.wait_event(e_side)
+        e_end.record(main)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e_end)
+
+    attn_all()
+    swap_out()
+    torch.cuda.synchronize()
+    reps = 3
+    t_a = sorted(span(True, False) for _ in range(reps))[reps // 2]
+    t_s = sorted(span(False, True) for _ in range(reps))[reps // 2]
+    t_b = sorted(span(True, True) for _ in range(reps))[reps // 2]
+    del cache, q, outs, host
+    torch.cuda.empty_cache()
+    return {"attn_ms": t_a, "swap_ms": t_s, "both_ms": t_b,
+            "swap_bytes": OVERLAP_SWAP_BLOCKS * g.block_bytes}
+
+
 # ------------------------------------------------------------------------- prefill
 PREFILL_LENS = [2048] * 4   # the reference's profiled prefill shape i2048b4
 
@@ -627,8 +706,8 @@ def main(argv=None):
     p.add_argument("--swap-seqs", type=int, default=32)
     p.add_argument("--pcie-blocks", type=int, default=64)
     p.add_argument("--only", default="all",
-                   help="comma list of append,attention,pack,defrag,gather,prefill,prepare,bm,"
-                        "calib or 'all'")
+                   help="comma list of append,attention,pack,defrag,gather,overlap,prefill,"
+                        "prepare,bm,calib or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU and "
@@ -643,13 +722,15 @@ def main(argv=None):
     torch.cuda.set_device(0)
     log(f"device: {torch.cuda.get_device_name(0)}")
     only = set(args.only.split(",")) if args.only != "all" else \
-        {"append", "attention", "pack", "defrag", "gather", "prefill", "prepare", "bm", "calib"}
+        {"append", "attention", "pack", "defrag", "gather", "overlap", "prefill", "prepare", "bm",
+         "calib"}
     timer = Timer()
     log(f"spin calibration: {timer.cycles_per_ms:.0f} cycles/ms")
     res = {}
     for name, fn in (("append", bench_append), ("attention", bench_attention),
                      ("gather", bench_gather), ("pack", bench_pack), ("defrag", bench_defrag),
-                     ("prefill", bench_prefill), ("prepare", bench_prepare),
+                     ("overlap", bench_overlap), ("prefill", bench_prefill),
+                     ("prepare", bench_prepare),
                      ("bm", bench_block_manager),
                      ("calib", bench_calib)):
         if name in only:
@@ -733,6 +814,17 @@ def main(argv=None):
                 "device_from_arrays": round(v["device_from_arrays"], 1),
                 "reference_host_loops": round(v["reference_host"], 1)}
             for k, v in res["prepare"].items()}
+    if "overlap" in res:
+        ov = res["overlap"]
+        hidden = (ov["attn_ms"] + ov["swap_ms"] - ov["both_ms"]) / min(ov["attn_ms"], ov["swap_ms"])
+        ops_out["swap_overlapped_with_attention"] = {
+            "workload": "28 layers of Qwen2.5-7B decode attention (128 seqs) on the compute "
+                        "stream; 128 scattered Qwen2.5-7B blocks (112 MiB) swapped out to "
+                        "pinned host on a side stream",
+            "attention_alone_ms": round(ov["attn_ms"], 3), "swap_alone_ms": round(ov["swap_ms"], 3),
+            "together_ms": round(ov["both_ms"], 3),
+            "swap_GB/s_alone": round(ov["swap_bytes"] / (ov["swap_ms"] * 1e-3) / 1e9, 1),
+            "fraction_of_shorter_hidden": round(hidden, 3)}
     if "prefill" in res:
         pf = res["prefill"]
         tf = pf["flops"] / (pf["attn_ms"] * 1e-3) / 1e12
