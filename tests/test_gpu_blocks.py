@@ -108,3 +108,58 @@ def test_empty_lists_are_noops(device):
     ops.swap([], [], False, cache, host)
     ops.defrag_blocks(cache, [], [])
     torch.cuda.synchronize()
+
+
+from hypothesis import given, settings, HealthCheck, strategies as st  # noqa: E402
+
+
+@st.composite
+def _swap_case(draw):
+    n_pool = draw(st.integers(4, 48))
+    n = draw(st.integers(1, n_pool // 2))
+    layers = draw(st.integers(1, 3))
+    heads = draw(st.sampled_from([1, 2, 4]))
+    dim = draw(st.sampled_from([8, 64, 128]))
+    perm = draw(st.permutations(range(n_pool)))
+    n_host = draw(st.integers(n, 2 * n + 8))
+    host_ids = draw(st.permutations(range(n_host)))[:n]
+    if draw(st.booleans()):  # runs of consecutive host ids (one DMA each)
+        start = draw(st.integers(0, n_host - n))
+        host_ids = list(range(start, start + n))
+    staging = draw(st.sampled_from(["auto", None, 1, 3]))
+    seed = draw(st.integers(0, 2 ** 31 - 1))
+    return n_pool, (layers, 2, 16, heads, dim), perm[:n], perm[n:2 * n], host_ids, n_host, \
+        staging, seed
+
+
+@settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.too_slow,
+                                                                  HealthCheck.function_scoped_fixture])
+@given(case=_swap_case())
+def test_swap_round_trip_property(device, case):
+    """Random pools, id permutations, host id runs and staging sizes: the
+    swap-out leaves host[host_ids[i]] == cache[src[i]] bit for bit, the swap-in
+    to fresh ids brings every block back, and untouched blocks keep their bytes."""
+    n_pool, shape, src, back, host_ids, n_host, staging, seed = case
+    rng = np.random.default_rng(seed)
+    bits = random_bits(rng, (n_pool, *shape), "fp16")
+    cache = to_device_bits(bits, "fp16", device)
+    host = torch.zeros((n_host, *shape), dtype=torch.float16, pin_memory=True)
+    stg = staging
+    if isinstance(staging, int):
+        stg = torch.empty(staging * ops.block_bytes_of(cache), dtype=torch.uint8, device=device)
+    ops.swap(src, host_ids, False, cache, host, staging=stg)
+    torch.cuda.synchronize()
+    hb = host.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(hb[host_ids], bits[src])
+    others = np.setdiff1d(np.arange(n_host), host_ids)
+    assert not hb[others].any()
+    ops.swap(host_ids, back, True, cache, host, staging=stg)
+    torch.cuda.synchronize()
+    got = to_bits(cache)
+    ref, host_ref = bits.copy(), np.zeros((n_host, *shape), dtype=np.uint16)
+    ko.swap_blocks(src, host_ids, False, ref, host_ref)
+    ko.swap_blocks(host_ids, back, True, ref, host_ref)
+    assert np.array_equal(got, ref)
+    assert np.array_equal(got[back], bits[src])
+    untouched = np.setdiff1d(np.arange(n_pool), back)
+    assert np.array_equal(got[untouched], bits[untouched])
