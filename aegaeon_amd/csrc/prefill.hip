@@ -78,6 +78,15 @@ struct PfOps<AEGKV_DTYPE_FP16> {
   }
 };
 
+// max(a, b, c) in one instruction.  (fmaxf on values the compiler cannot
+// prove canonical, such as MFMA results, costs a v_max_f32 x, x per operand
+// first; the scores here are never signalling NaNs.)
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // {lo16(a), lo16(b)} and {hi16(a), hi16(b)} (v_perm_b32: src1 = bytes 0-3)
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x05040100u);
@@ -182,10 +191,12 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
   };
   auto store_v = [&](int kt, int slot) {
     if (t >= VTHREADS) return;
-    u32x4 x[4];
+    if (kt * kPfKTile + kPfKTile > len) {  // last tile only (uniform)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)  // keys past the end: 0 (P is 0 there, V may be NaN)
-      x[i] = kt * kPfKTile + 4 * vq + i < len ? vreg[i] : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < 4; ++i)  // keys past the end: 0 (P is 0 there, V may be NaN)
+        if (kt * kPfKTile + 4 * vq + i >= len) vreg[i] = u32x4{0, 0, 0, 0};
+    }
+    const u32x4* x = vreg;
     uint8_t* vt = lds + 2 * K_BYTES + slot * V_BYTES + vpos * 2;
 #pragma unroll
     for (int wd = 0; wd < 4; ++wd) {  // dims 2 wd (low halves) and 2 wd + 1 (high)
@@ -236,13 +247,15 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
 
   // softmax of a masked S^T tile and O^T += V^T . P^T (V stage kt & 1)
   auto softmax_pv = [&](int kt, f32x16 (&s)[2]) {
-    float bm = -INFINITY;  // raw-score max (the scale is positive)
+    float bm = max3(s[0][0], s[0][1], s[0][2]);  // raw-score max (the scale is positive)
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2)
-        bm = __builtin_fmaxf(bm, __builtin_fmaxf(s[sb][i], s[sb][i + 1]));
-    bm = fmaxf(bm, __shfl_xor(bm, 32)) * a.scale_log2;
+    for (int i = 3; i < 31; i += 2) {
+      const int sb = i >> 4, e = i & 15;
+      bm = max3(bm, s[sb][e], s[(i + 1) >> 4][(i + 1) & 15]);
+    }
+    bm = max3(bm, s[1][15], s[1][15]);  // all 32 of this lane's scores
+    const float pm = __shfl_xor(bm, 32);  // the partner lane's (same query)
+    bm = max3(bm, pm, pm) * a.scale_log2;
     if (__builtin_amdgcn_ballot_w64(bm > m + kPfRescaleSlack)) {
       const float mn = fmaxf(m, bm);
       const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 while m = -inf
