@@ -37,6 +37,7 @@ int check_disjoint(const int64_t* a, int64_t na, const int64_t* b, int64_t nb);
 struct DeviceState {
   int device = -1;
   int num_cu = 0;
+  int max_lds = 0;  // bytes of LDS one workgroup may use
   std::mutex mu;
   int64_t* host_ring = nullptr;
   int64_t* dev_ring = nullptr;

@@ -26,7 +26,11 @@
 //
 // Inside a workgroup, wave w handles kv head grp * 4 + w, and all
 // G = Hq / Hkv query heads of that kv head are processed together, so each K/V
-// byte is read from HBM exactly once per decode step.
+// byte is read from HBM exactly once per decode step.  A wave streams the
+// blocks of its whole range through one register pipeline, across sequence
+// boundaries, and keeps the pieces it finishes in LDS until the stream ends
+// (attend_items); one piece per sequence start and a pipeline drain per
+// piece measured ~3.8 us each, against ~1 us for a switch in the stream.
 //
 // Per 16-token block (block_size 16), with lane l = 16*g + j:
 //   S^T[16 tok x 16 heads] = K[16 x D] . Q^T[D x 16]  -> D/32 MFMA 16x16x32
@@ -42,9 +46,9 @@
 //     Lane (j, g) loads V rows 4g..4g+3, dims [D/16*j, +D/16); tile t of the
 //     output holds dims D/16*i + t for A-row i, so output lane (j, g) owns head
 //     j, dims D/16*(4g+r) + t.
-// The block ids of a segment are loaded 64 at a time, one per lane, and read
-// with readlane; a rolling register pipeline keeps pipeline_depth - 1 blocks of K/V
-// in flight while one is computed.
+// The block ids of a range are loaded 64 at a time, one per lane, and read
+// with readlane; a rolling register pipeline keeps pipeline_depth - 1 blocks of
+// K/V in flight while one is computed.
 #include <algorithm>
 #include <cmath>
 #include <utility>
@@ -65,12 +69,15 @@ constexpr int kHeadsPerGroup = 4;   // waves (kv heads) per workgroup
 constexpr int kMaxBatch = 2048;     // sequences per launch (LDS prefix sums); larger
                                     // batches are launched in chunks
 constexpr int kMaxWorkgroups = 8192;  // bound of n_workgroups
+constexpr int kMaxStage = 4;          // finished pieces a wave stages in LDS
+constexpr int kStageBudget = 64 * 1024;  // dynamic LDS of a workgroup, scan arrays included
 constexpr int kScanPerThread = kMaxBatch / (64 * kHeadsPerGroup);
-// Cost of starting a sequence piece (block ids and q loaded, pipeline
-// primed) in units of one block: the partition balances blocks plus this
-// charge per sequence, so a workgroup that holds several short sequences gets
-// correspondingly fewer blocks (measured ~2 blocks on the Qwen2.5-7B batch).
-constexpr int kSegmentCost = 2;
+// Cost of switching the block stream to a new sequence (its piece staged,
+// its query swapped in) in units of one block: the partition balances blocks
+// plus this charge per sequence, so a workgroup that holds several short
+// sequences gets correspondingly fewer blocks (measured ~1 block on the
+// Qwen2.5-7B batch; 2 and 0 were slower).
+constexpr int kSegmentCost = 1;
 
 // Cost units of a sequence of `len` tokens: its blocks plus the start charge.
 __device__ __forceinline__ int cost_units(int len) {
@@ -150,6 +157,8 @@ struct AttnArgs {
   int4* desc;           // [n_wg] cut sequence ending in each workgroup: (b, grp, w0, npieces)
   float* part_o;        // [slots][hpg][D]
   float2* part_ml;      // [slots][hpg] (running max in log2 units, sum)
+  int32_t stage_slots;  // finished pieces a wave holds in LDS (0: stored at once)
+  int32_t stage_off;    // byte offset of the staging area in dynamic LDS
 };
 
 // Workspace layout of one launch: the workgroups' descriptors, then the
@@ -288,103 +297,45 @@ __device__ __forceinline__ bool unrolled_steps(F&& f) {
   return unrolled_steps_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// One piece of a sequence for one kv head: blocks [j0, j1) of sequence b.
-// `complete` (the piece is the whole sequence) writes the normalised output,
-// otherwise the partial goes to `slot`.
-template <int DT, int D, int NBUF>
-__device__ __forceinline__ void attend_segment(const AttnArgs& a, int b, int h, int j0, int j1,
-                                               int len, bool complete, int64_t slot, int hl0) {
+// Largest b in [0, batch) with cum[b] <= i, for 0 <= i < cum[batch] and cum
+// non-decreasing.  Over block counts this is the (non-empty) sequence that
+// holds block item i; over positions, the sequence that holds position i.
+__device__ __forceinline__ int seq_at(const int32_t* cum, int batch, int i) {
+  int lo = 0, hi = batch;  // cum[lo] <= i < cum[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cum[mid] <= i) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Finished pieces.  Lane (j, g) holds query head j, dims
+// [4*DPL*g, 4*DPL*g + 4*DPL) with dim offset DPL*r + t <- acc[t][r].  A
+// whole sequence is written normalised to `out`; a piece of a cut sequence as
+// its fp32 partial and (max, sum) for the merge.  Inside the block stream a
+// piece goes to an LDS record instead (lane record: D bytes of partial or
+// D/2 of output, then (max, sum)); global stores there would join the K/V
+// loads in the vector-memory counter and every wait after them would wait for
+// the stores as well.  The records are written out when the wave's stream
+// ends, or when its stage_slots records are full.
+template <int D>
+constexpr int stage_record_bytes() { return D + 16; }
+// D = 256 keeps direct stores: its registers leave no room for the records.
+template <int D>
+constexpr bool stages_pieces() { return D <= 128; }
+
+template <int DT, int D>
+__device__ __forceinline__ void store_piece(const AttnArgs& a, const f32x4* acc, float m,
+                                            float lt, int b, int hq, bool complete, int64_t slot,
+                                            int hl0) {
   using E = Elem<DT>;
-  constexpr int KS = D / 32;
   constexpr int DPL = D / 16;
   constexpr int VW = D / 32;
   const int lane = threadIdx.x & 63;
   const int j = lane & 15, g = lane >> 4;
-  const bool head_ok = j < a.group;
-  const int hq = h * a.group + j;
-
-
-  f32x4 acc[DPL];
-#pragma unroll
-  for (int t = 0; t < DPL; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, lsum = 0.f;
-
-  const int64_t row = (int64_t)a.n_kv_heads * D;
-  const uint16_t* kh = a.kc + (int64_t)h * D + (int64_t)j * row + 8 * g;
-  const uint16_t* vh = a.vc + (int64_t)h * D + (int64_t)(4 * g) * row + DPL * j;
-  const int32_t* bt = a.block_tables + (int64_t)b * a.max_blocks;
-
-  // Block ids are loaded one 64-block chunk ahead, unconditionally (clamped
-  // index, masked at use) so that no load sits under a branch; the first
-  // chunk's are loaded before q: the waits are in issue order, so the K/V
-  // loads that need the ids can start while q is in flight.
-  int id_next = bt[min(j0 + lane, j1 - 1)];
-  // Lanes past the group load the group's first head: every head column of
-  // the products and of the softmax is independent and only real heads are
-  // written, so no select has to wait for q here.
-  u32x4 qv[KS];
-  {
-    const uint16_t* qp = a.q + (int64_t)b * a.q_bstride + (int64_t)(head_ok ? hq : h * a.group) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qv[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks + 8 * g);
-  }
-
-  for (int c0 = j0; c0 < j1; c0 += 64) {
-    const int nb = min(64, j1 - c0);
-    // block ids of this chunk, one per lane; ids outside the pool become -1
-    const int id = id_next;
-    const int my_id = (lane < nb && id >= 0 && id < a.n_blocks) ? id : -1;
-    id_next = bt[min(c0 + 64 + lane, j1 - 1)];
-    // Rolling register pipeline of NBUF blocks: buffer k holds block i = it + k;
-    // as soon as block i is computed, its buffer is refilled with block
-    // i + NBUF, so NBUF - 1 blocks stay in flight while a block is computed and
-    // the loads carried across the loop's back edge keep HBM busy between
-    // iterations.  The loop body is unrolled by NBUF, so every buffer keeps its
-    // registers across the back edge.  Inside the loop every load is issued
-    // unconditionally and no path leaves the body early (a refill past the
-    // chunk re-reads its last block, an L2 hit, and is never computed): the
-    // in-order vmcnt accounting then stays exact across the back edge and each
-    // wait covers only the buffer about to be computed.  The last nb % NBUF
-    // blocks are computed after the loop, which issues no further loads.  An
-    // unreadable id loads block 0 and is masked (the host guarantees
-    // n_blocks >= 1).
-    const int last = nb - 1;
-    const int nfull = nb - nb % NBUF;
-    KVRegs<D> buf[NBUF];
-    int ids[NBUF];
-    unrolled_steps<NBUF>([&](auto kc) {
-      constexpr int k = decltype(kc)::value;
-      ids[k] = __builtin_amdgcn_readlane(my_id, min(k, last));
-      load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
-      return false;
-    });
-    for (int it = 0; it < nfull; it += NBUF) {
-      unrolled_steps<NBUF>([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        const int i = it + k;
-        compute_block<DT, D>(buf[k], qv, acc, m, lsum, (c0 + i) * kBlockSize,
-                             ids[k] >= 0 ? len : 0, g, a.scale_log2);
-        ids[k] = __builtin_amdgcn_readlane(my_id, min(i + NBUF, last));
-        load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
-        return false;
-      });
-    }
-    unrolled_steps<NBUF>([&](auto kc) {
-      constexpr int k = decltype(kc)::value;
-      const int i = nfull + k;
-      if (i >= nb) return true;
-      compute_block<DT, D>(buf[k], qv, acc, m, lsum, (c0 + i) * kBlockSize,
-                           ids[k] >= 0 ? len : 0, g, a.scale_log2);
-      return false;
-    });
-  }
-
-  float lt = lsum + __shfl_xor(lsum, 16);
-  lt += __shfl_xor(lt, 32);
-
-  // lane holds head j, dims [4*DPL*g, 4*DPL*g + 4*DPL): dim offset DPL*r + t <- acc[t][r]
   const int d0 = 4 * DPL * g;
-  if (!head_ok) return;
   if (complete) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     uint16_t* op = a.out + (int64_t)b * a.out_bstride + (int64_t)hq * D + d0;
@@ -416,30 +367,234 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int b, int h, 
   }
 }
 
+// LDS record <-> accumulators (the record keeps the fp32 state; the output
+// is normalised and rounded when it is written out, as store_piece does)
+template <int D>
+__device__ __forceinline__ void put_record(uint8_t* rec, const f32x4* acc, float m, float lt) {
+  constexpr int DPL = D / 16;
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) *reinterpret_cast<f32x4*>(rec + 16 * t) = acc[t];
+  *reinterpret_cast<float2*>(rec + D) = make_float2(m, lt);
+}
+template <int D>
+__device__ __forceinline__ void get_record(const uint8_t* rec, f32x4* acc, float& m, float& lt) {
+  constexpr int DPL = D / 16;
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) acc[t] = *reinterpret_cast<const f32x4*>(rec + 16 * t);
+  const float2 ml = *reinterpret_cast<const float2*>(rec + D);
+  m = ml.x;
+  lt = ml.y;
+}
+
+// One wave's share of a workgroup's range within kv-head group `grp`: block
+// items [i0, i1) of the group, item i being block i - bcum[b] of the sequence
+// b with bcum[b] <= i < bcum[b + 1], for kv head grp * 4 + wave.
+//
+// The items are streamed through one rolling register pipeline of NBUF
+// blocks whatever the sequence boundaries: buffer k holds item i0 + it + k;
+// as soon as it is computed the buffer is refilled with the item NBUF
+// further on, so NBUF - 1 blocks stay in flight across the end of one
+// sequence and the start of the next.  A sequence piece that ends costs its
+// output stores and the switch to the next sequence, whose query was loaded
+// when the previous switch happened.  Inside the loop every K/V load is
+// issued unconditionally (a refill past the range re-reads its last block,
+// an L2 hit that is never computed).  Block ids come 64 items at a time, one
+// per lane, with the next 64 loaded a chunk ahead; an unreadable id loads
+// block 0 and is masked (the host guarantees n_blocks >= 1).
+template <int DT, int D, int NBUF>
+__device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s_bcum,
+                                             const int32_t* s_len, uint8_t* stage, int4* meta,
+                                             int grp, int b0, int i0, int i1) {
+  constexpr int KS = D / 32;
+  constexpr int DPL = D / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = grp * kHeadsPerGroup + wave;
+  if (h >= a.n_kv_heads) return;  // wave past the last kv head (uniform)
+  const int j = lane & 15, g = lane >> 4;
+  const bool head_ok = j < a.group;
+  const int hq = h * a.group + j;
+  const int hl0 = wave * a.group;
+  const int64_t row = (int64_t)a.n_kv_heads * D;
+  const uint16_t* kh = a.kc + (int64_t)h * D + (int64_t)j * row + 8 * g;
+  const uint16_t* vh = a.vc + (int64_t)h * D + (int64_t)(4 * g) * row + DPL * j;
+
+  // the sequence being computed: bc, whose block 0 is item `first`, with
+  // items up to cend in range
+  int bc = b0;
+  int first = uni(s_bcum[bc]);
+  int cend = min(uni(s_bcum[bc + 1]), i1);
+  int len = uni(s_len[bc]);
+  bool complete = first >= i0 && cend == uni(s_bcum[bc + 1]);
+
+  // block id of item i (clamped into the range), one lane per item; bh is a
+  // sequence at or before the item's (the item's own or the next one are
+  // checked before a search)
+  auto item_id = [&](int i, int bh) -> int {
+    i = min(i, i1 - 1);
+    int b = bh;
+    if (s_bcum[b + 1] <= i) b = s_bcum[b + 2] > i ? b + 1 : seq_at(s_bcum, a.batch, i);
+    return a.block_tables[(int64_t)b * a.max_blocks + (i - s_bcum[b])];
+  };
+  int id_cur = item_id(i0 + lane, bc);       // items [cbase, cbase + 64)
+  int id_nxt = item_id(i0 + 64 + lane, bc);  // items [cbase + 64, cbase + 128)
+  int cbase = i0;
+  // id of item i >= cbase (uniform): rotates the chunks when i leaves the
+  // current one; ids outside the pool become -1
+  auto id_at = [&](int i) -> int {
+    if (i - cbase >= 64) {
+      id_cur = id_nxt;
+      cbase += 64;
+      id_nxt = item_id(cbase + 64 + lane, bc);
+    }
+    const int id = __builtin_amdgcn_readlane(id_cur, i - cbase);
+    return (id >= 0 && id < a.n_blocks) ? id : -1;
+  };
+  // query rows of sequence b (lanes past the group load the group's first
+  // head: every head column is independent and only real heads are written)
+  auto load_q = [&](int b, u32x4* qv) {
+    const uint16_t* qp =
+        a.q + (int64_t)b * a.q_bstride + (int64_t)(head_ok ? hq : h * a.group) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qv[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks + 8 * g);
+  };
+  // the next non-empty sequence after b (one exists while items remain)
+  auto next_seq = [&](int b) -> int {
+    ++b;
+    while (uni(s_bcum[b + 1]) == uni(s_bcum[b])) ++b;
+    return b;
+  };
+
+  u32x4 qv[KS], qn[KS];
+  load_q(bc, qv);
+  int bn = cend < i1 ? next_seq(bc) : bc;
+  load_q(bn, qn);
+
+  f32x4 acc[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, lsum = 0.f;
+
+  // staged pieces: meta[s] = (b, complete, partial slot)
+  const int rec_bytes = stage_record_bytes<D>();
+  const int slot_bytes = a.group * 4 * rec_bytes;
+  uint8_t* my_rec = stage + (j * 4 + g) * rec_bytes;
+  int nstaged = 0;
+  auto flush = [&]() {
+    if constexpr (!stages_pieces<D>()) return;
+    for (int s = 0; s < nstaged; ++s) {
+      const int4 md = meta[s];
+      f32x4 o[DPL];
+      float mm, lt;
+      if (head_ok) {
+        get_record<D>(my_rec + s * slot_bytes, o, mm, lt);
+        store_piece<DT, D>(a, o, mm, lt, uni(md.x), hq, uni(md.y) != 0, uni(md.z), hl0);
+      }
+    }
+    nstaged = 0;
+  };
+
+  int ic = i0;  // next item to compute
+  auto compute = [&](KVRegs<D>& r, int id) {
+    compute_block<DT, D>(r, qv, acc, m, lsum, (ic - first) * kBlockSize, id >= 0 ? len : 0, g,
+                         a.scale_log2);
+    if (++ic == cend) {  // the piece of sequence bc in this range ends (uniform)
+      float lt = lsum + __shfl_xor(lsum, 16);
+      lt += __shfl_xor(lt, 32);
+      const int pslot = (int)blockIdx.x + grp * a.batch + bc;
+      if (stages_pieces<D>() && a.stage_slots > 0) {
+        if (nstaged == a.stage_slots) flush();
+        if (head_ok) put_record<D>(my_rec + nstaged * slot_bytes, acc, m, lt);
+        if (lane == 0) meta[nstaged] = make_int4(bc, complete ? 1 : 0, pslot, 0);
+        ++nstaged;
+      } else if (head_ok) {
+        store_piece<DT, D>(a, acc, m, lt, bc, hq, complete, pslot, hl0);
+      }
+      if (ic < i1) {
+        bc = bn;
+        first = uni(s_bcum[bc]);
+        cend = min(uni(s_bcum[bc + 1]), i1);
+        len = uni(s_len[bc]);
+        complete = cend == uni(s_bcum[bc + 1]);  // it starts in range
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qv[ks] = qn[ks];
+        bn = cend < i1 ? next_seq(bc) : bc;
+        load_q(bn, qn);
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m = -INFINITY;
+        lsum = 0.f;
+      }
+    }
+  };
+
+  const int n = i1 - i0;
+  const int nfull = n - n % NBUF;
+  KVRegs<D> buf[NBUF];
+  int ids[NBUF];
+  unrolled_steps<NBUF>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    ids[k] = id_at(min(i0 + k, i1 - 1));
+    load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
+    return false;
+  });
+  for (int it = 0; it < nfull; it += NBUF) {
+    unrolled_steps<NBUF>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      compute(buf[k], ids[k]);
+      ids[k] = id_at(min(i0 + it + k + NBUF, i1 - 1));
+      load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
+      return false;
+    });
+  }
+  unrolled_steps<NBUF>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    if (nfull + k >= n) return true;
+    compute(buf[k], ids[k]);
+    return false;
+  });
+  flush();
+}
+
 // Workgroup that holds position P of the flattened range (the largest w with
 // floor(w * total / n_act) <= P; n_act <= total, so every range is non-empty).
+// floor(num / den) for 0 <= num, den < 2^52 (the host bounds every operand
+// below by that): the correctly rounded double quotient is within one of the
+// exact one, and one integer step corrects it.  A fraction of the cost of a
+// 64-bit integer division, which the startup of every workgroup needs several
+// of.
+__device__ __forceinline__ int64_t div_floor(int64_t num, int64_t den) {
+  int64_t q = (int64_t)((double)num / (double)den);
+  if (q * den > num) --q;
+  else if ((q + 1) * den <= num) ++q;
+  return q;
+}
+
 __device__ __forceinline__ int64_t owner_of(int64_t P, int64_t total, int64_t n_act) {
-  return ((P + 1) * n_act - 1) / total;
+  return div_floor((P + 1) * n_act - 1, total);
 }
 
 template <int DT, int D, int NBUF>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, D >= 256 ? 1 : 2) void
 paged_decode_attention_kernel(AttnArgs a) {
-  extern __shared__ int32_t s_mem[];  // cum[batch + 1], then len[batch]
-  __shared__ int32_t s_wave_tot[kHeadsPerGroup];
+  // cum[batch + 1] (positions), len[batch], bcum[batch + 1] (blocks)
+  extern __shared__ int32_t s_mem[];
+  __shared__ int32_t s_wave_tot[2][kHeadsPerGroup];
+  __shared__ int32_t s_find[2];
+  __shared__ int4 s_meta[kHeadsPerGroup][kMaxStage];
   int32_t* s_cum = s_mem;
   int32_t* s_len = s_mem + a.batch + 1;
+  int32_t* s_bcum = s_len + a.batch;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
 
-  // Cost prefix sums of the batch: thread t owns sequences
+  // Prefix sums of the batch's positions and blocks: thread t owns sequences
   // [t * per, t * per + per); a wave scan plus the wave totals give each
-  // thread its exclusive offset.
+  // thread its exclusive offsets.
   {
     const int per = (a.batch + 64 * kHeadsPerGroup - 1) / (64 * kHeadsPerGroup);
     const int b0 = tid * per;
     int lens[kScanPerThread];
-    int cnt = 0;
+    int cnt = 0, bcnt = 0;
     // all loads issued before any is used (clamped index, masked after)
 #pragma unroll
     for (int k = 0; k < kScanPerThread; ++k) lens[k] = a.seq_lens[min(b0 + k, a.batch - 1)];
@@ -447,27 +602,42 @@ paged_decode_attention_kernel(AttnArgs a) {
     for (int k = 0; k < kScanPerThread; ++k) {
       lens[k] = (k < per && b0 + k < a.batch) ? min(max(lens[k], 0), a.max_seq_len) : 0;
       cnt += cost_units(lens[k]);
+      bcnt += (lens[k] + kBlockSize - 1) / kBlockSize;
     }
-    int x = cnt;
+    int x = cnt, y = bcnt;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o);
-      if (lane >= o) x += y;
+      const int xu = __shfl_up(x, o), yu = __shfl_up(y, o);
+      if (lane >= o) {
+        x += xu;
+        y += yu;
+      }
     }
-    if (lane == 63) s_wave_tot[wave] = x;
+    if (lane == 63) {
+      s_wave_tot[0][wave] = x;
+      s_wave_tot[1][wave] = y;
+    }
     __syncthreads();
-    int base = 0;
-    for (int w = 0; w < wave; ++w) base += s_wave_tot[w];
-    int excl = base + x - cnt;
+    int base = 0, bbase = 0;
+    for (int w = 0; w < wave; ++w) {
+      base += s_wave_tot[0][w];
+      bbase += s_wave_tot[1][w];
+    }
+    int excl = base + x - cnt, bexcl = bbase + y - bcnt;
 #pragma unroll
     for (int k = 0; k < kScanPerThread; ++k) {
       if (k < per && b0 + k < a.batch) {
         s_cum[b0 + k] = excl;
+        s_bcum[b0 + k] = bexcl;
         s_len[b0 + k] = lens[k];
         excl += cost_units(lens[k]);
+        bexcl += (lens[k] + kBlockSize - 1) / kBlockSize;
       }
     }
-    if (tid == 64 * kHeadsPerGroup - 1) s_cum[a.batch] = base + x;
+    if (tid == 64 * kHeadsPerGroup - 1) {
+      s_cum[a.batch] = base + x;
+      s_bcum[a.batch] = bbase + y;
+    }
     __syncthreads();
   }
   // Empty sequences have no positions: workgroup b % n_wg writes their zeros.
@@ -487,47 +657,50 @@ paged_decode_attention_kernel(AttnArgs a) {
     if (tid == 0) a.desc[blockIdx.x] = make_int4(-1, 0, 0, 0);
     return;
   }
-  bool first_piece = true;  // the range's first piece is the only one that can end a cut sequence
-  int64_t P = (int64_t)blockIdx.x * total / n_act;
-  const int64_t p_end = (int64_t)(blockIdx.x + 1) * total / n_act;
+  int64_t P = div_floor((int64_t)blockIdx.x * total, n_act);
+  const int64_t p_end = div_floor((int64_t)(blockIdx.x + 1) * total, n_act);
   // Every value below is uniform over the workgroup.  A sequence occupies
-  // positions [s_cum[b], s_cum[b + 1]): kSegmentCost charge positions, then
-  // one per block.
-  while (P < p_end) {
-    const int grp = (int)(P / W);
-    const int p = (int)(P - (int64_t)grp * W);
-    int lo = 0, hi = a.batch;  // s_cum[lo] <= p < s_cum[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_cum[mid] <= p) lo = mid; else hi = mid;
-    }
-    const int b = lo;
-    const int first = s_cum[b] + kSegmentCost;  // position of block 0
-    if (p < first) {  // charge positions hold no block
-      P += first - p;
-      continue;
-    }
-    const int nblk = s_cum[b + 1] - first;
-    const int j0 = p - first;
-    const int j1 = (int)min((int64_t)nblk, (int64_t)j0 + (p_end - P));
-    // pieces of (grp, b): the owners of its block positions
+  // positions [s_cum[b], s_cum[b + 1]) of its group: kSegmentCost charge
+  // positions, then one per block.
+  uint8_t* stage = reinterpret_cast<uint8_t*>(s_mem) + a.stage_off +
+                   wave * a.stage_slots * a.group * 4 * stage_record_bytes<D>();
+  bool first_pass = true;
+  while (P < p_end) {  // one pass per kv-head group the range touches
+    const int grp = (int)div_floor(P, W);
     const int64_t pbase = (int64_t)grp * W;
-    const int64_t w0 = owner_of(pbase + first, total, n_act);
-    const int64_t w1 = owner_of(pbase + s_cum[b + 1] - 1, total, n_act);
-    const int h = grp * kHeadsPerGroup + wave;
-    if (first_piece) {
-      first_piece = false;
-      if (tid == 0)
-        a.desc[blockIdx.x] = (w0 != w1 && j1 == nblk) ? make_int4(b, grp, (int)w0, (int)(w1 - w0 + 1))
-                                                      : make_int4(-1, 0, 0, 0);
+    const int64_t q_end = min(p_end, pbase + W);
+    const int p0 = (int)(P - pbase), p1 = (int)(q_end - pbase);
+    // the sequences holding positions p0 and p1 (p1 < W), every thread
+    // testing its own sequences at once
+    for (int b = tid; b < a.batch; b += 64 * kHeadsPerGroup) {
+      const int lo = s_cum[b], hi = s_cum[b + 1];
+      if (lo <= p0 && p0 < hi) s_find[0] = b;
+      if (lo <= p1 && p1 < hi) s_find[1] = b;
     }
-    if (h < a.n_kv_heads)
-      attend_segment<DT, D, NBUF>(a, b, h, j0, j1, s_len[b], w0 == w1,
-                                  (int64_t)blockIdx.x + (int64_t)grp * a.batch + b,
-                                  wave * a.group);
-    P += j1 - j0;
+    __syncthreads();
+    // block items before position p of sequence b
+    auto items_before = [&](int b, int p) -> int {
+      const int nblk = s_bcum[b + 1] - s_bcum[b];
+      return s_bcum[b] + min(max(p - s_cum[b] - kSegmentCost, 0), nblk);
+    };
+    const int b0 = s_find[0];
+    const int i0 = items_before(b0, p0);
+    const int i1 = p1 == (int)W ? s_bcum[a.batch] : items_before(s_find[1], p1);
+    if (first_pass) {
+      // The range's first piece is the only one that can end a cut sequence:
+      // describe it for the merge when it does.
+      const int64_t w0 = owner_of(pbase + s_cum[b0] + kSegmentCost, total, n_act);
+      const int64_t w1 = owner_of(pbase + s_cum[b0 + 1] - 1, total, n_act);
+      if (tid == 0)
+        a.desc[blockIdx.x] = (w0 != w1 && w1 == (int64_t)blockIdx.x)
+                                 ? make_int4(b0, grp, (int)w0, (int)(w1 - w0 + 1))
+                                 : make_int4(-1, 0, 0, 0);
+      first_pass = false;
+    }
+    if (i1 > i0) attend_items<DT, D, NBUF>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0, i0, i1);
+    P = q_end;
+    __syncthreads();  // s_find is rewritten by the next pass
   }
-  if (first_piece && tid == 0) a.desc[blockIdx.x] = make_int4(-1, 0, 0, 0);
 }
 
 // Merge the pieces of the cut sequence whose last block workgroup
@@ -630,7 +803,17 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(
   }
 }
 
-size_t lds_bytes(int32_t batch) { return (size_t)(2 * batch + 1) * sizeof(int32_t); }
+// Dynamic LDS of the main kernel: the scan arrays, then (16-byte aligned) the
+// staging records of the four waves.  Sets a.stage_slots and a.stage_off.
+size_t lds_bytes(AttnArgs& a, int max_lds) {
+  const int64_t scan = ((int64_t)(3 * a.batch + 2) * (int64_t)sizeof(int32_t) + 15) / 16 * 16;
+  const int64_t per_slot = (int64_t)kHeadsPerGroup * a.group * 4 * (a.head_dim + 16);
+  const int64_t budget = std::min<int64_t>(kStageBudget, max_lds) - scan;
+  a.stage_off = (int32_t)scan;
+  a.stage_slots = a.head_dim > 128 ? 0
+                  : (int32_t)std::max<int64_t>(0, std::min<int64_t>(kMaxStage, budget / per_slot));
+  return (size_t)(scan + a.stage_slots * per_slot);
+}
 
 // Workgroups of the main kernel for one launch: one per CU (measured on the
 // Qwen2.5-7B batch: one workgroup of four waves per CU with three blocks in
@@ -647,6 +830,15 @@ int workgroups_for(int32_t requested, int* n_wg) {
   return AEGKV_OK;
 }
 
+// The kernel's position arithmetic: a group's positions W (bounded by
+// chunk * (blocks + kSegmentCost)) must fit int32, and the products of the
+// range arithmetic (total * n_wg, total = W * n_groups) must stay below 2^52
+// for div_floor.
+bool positions_fit(int64_t chunk, int64_t nblk_max, int64_t n_groups, int64_t n_wg) {
+  const int64_t w_max = chunk * (nblk_max + kSegmentCost);
+  return w_max < (1ll << 31) && w_max * n_groups * n_wg < (1ll << 52);
+}
+
 template <int DT, int D, int KI>
 int launch_combine(const AttnArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI>), dim3(a.n_wg, kHeadsPerGroup),
@@ -656,9 +848,9 @@ int launch_combine(const AttnArgs& a, hipStream_t stream) {
 }
 
 template <int DT, int D>
-int launch_attention(const AttnArgs& a, hipStream_t stream) {
+int launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
   hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>()>), dim3(a.n_wg),
-                     dim3(64 * kHeadsPerGroup), lds_bytes(a.batch), stream, a);
+                     dim3(64 * kHeadsPerGroup), lds, stream, a);
   AEGKV_HIP_TRY(hipGetLastError());
   const int items = a.group * (D / 4);  // <= 16 * D / 4
   if (items <= 64) return launch_combine<DT, D, 1>(a, stream);
@@ -688,13 +880,13 @@ int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_h
     return AEGKV_ERR_UNSUPPORTED;
   if (batch == 0) return 0;
   const int32_t chunk = std::min(batch, kMaxBatch);
-  if ((int64_t)chunk * (((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize) >= (1ll << 31))
-    return AEGKV_ERR_UNSUPPORTED;
   int n_wg = 0;
   const int rc = workgroups_for(n_workgroups, &n_wg);
   if (rc) return rc > 0 ? AEGKV_ERR_RUNTIME : rc;
   const int32_t group = n_q_heads / n_kv_heads;
   const int32_t n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  if (!positions_fit(chunk, ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize, n_groups, n_wg))
+    return AEGKV_ERR_UNSUPPORTED;
   return workspace_layout(chunk, kHeadsPerGroup * group, head_dim, n_wg, n_groups).total;
 }
 
@@ -725,12 +917,12 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
   const int64_t nblk_max = ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize;
   if (nblk_max > max_blocks) return AEGKV_ERR_INVALID_ARG;
   const int32_t chunk = std::min(batch, kMaxBatch);
-  if ((int64_t)chunk * nblk_max >= (1ll << 31)) return AEGKV_ERR_UNSUPPORTED;
   int n_wg = 0;
   int rc = workgroups_for(n_workgroups, &n_wg);
   if (rc) return rc;
   const int32_t group = n_q_heads / n_kv_heads;
   const int32_t n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  if (!positions_fit(chunk, nblk_max, n_groups, n_wg)) return AEGKV_ERR_UNSUPPORTED;
   const WorkspaceLayout lay =
       workspace_layout(chunk, kHeadsPerGroup * group, head_dim, n_wg, n_groups);
   if (!workspace || workspace_bytes < (uint64_t)lay.total) return AEGKV_ERR_WORKSPACE;
@@ -758,6 +950,9 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
   a.part_o = reinterpret_cast<float*>(ws + lay.desc_bytes + lay.ml_bytes);
   hipStream_t st = (hipStream_t)stream;
   const bool bf = dtype == AEGKV_DTYPE_BF16;
+  DeviceState* ds = nullptr;
+  rc = current_device_state(&ds);
+  if (rc) return rc;
   // Batches above kMaxBatch run as consecutive launches of kMaxBatch sequences
   // that share the workspace (stream order keeps them apart).
   for (int32_t c = 0; c < batch; c += kMaxBatch) {
@@ -766,13 +961,14 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
     a.out = static_cast<uint16_t*>(out) + (int64_t)c * out_batch_stride;
     a.block_tables = block_tables + (int64_t)c * max_blocks;
     a.seq_lens = seq_lens + c;
+    const size_t lds = lds_bytes(a, ds->max_lds);
     switch (head_dim) {
-      case 64: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 64>(a, st)
-                       : launch_attention<AEGKV_DTYPE_FP16, 64>(a, st); break;
-      case 128: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 128>(a, st)
-                        : launch_attention<AEGKV_DTYPE_FP16, 128>(a, st); break;
-      default: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 256>(a, st)
-                       : launch_attention<AEGKV_DTYPE_FP16, 256>(a, st); break;
+      case 64: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 64>(a, lds, st)
+                       : launch_attention<AEGKV_DTYPE_FP16, 64>(a, lds, st); break;
+      case 128: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 128>(a, lds, st)
+                        : launch_attention<AEGKV_DTYPE_FP16, 128>(a, lds, st); break;
+      default: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 256>(a, lds, st)
+                       : launch_attention<AEGKV_DTYPE_FP16, 256>(a, lds, st); break;
     }
     if (rc) return rc;
   }

@@ -67,6 +67,8 @@ int current_device_state(DeviceState** out) {
   auto* ds = new DeviceState();
   ds->device = dev;
   hipError_t e = hipDeviceGetAttribute(&ds->num_cu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess)
+    e = hipDeviceGetAttribute(&ds->max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (e != hipSuccess) {
     delete ds;
     return (int)e;
