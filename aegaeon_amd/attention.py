@@ -188,17 +188,70 @@ def _cached_workspace(device: torch.device, stream: int, nbytes: int) -> torch.T
         return ws
 
 
+def _int32_dense(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
+
+
+class DecodePlan:
+    """The attention's work split for one decode step (aegkv_paged_decode_plan):
+    which blocks each workgroup takes and the block ids in that order, built
+    once from the step's block tables and lengths and passed to every layer's
+    :func:`paged_decode_attention` (``plan=``).  The tables and lengths must
+    not change while the plan is in use; the plan keeps references to them.
+    Batches above 2048 sequences are not planned (AegkvError)."""
+
+    def __init__(self, block_tables: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int,
+                 n_kv_heads: int, n_workgroups: int = 0):
+        if not block_tables.is_cuda or not seq_lens.is_cuda or block_tables.dim() != 2:
+            raise ValueError("block_tables [B, max_blocks] and seq_lens [B] must be GPU tensors")
+        self.block_tables = _int32_dense(block_tables)
+        self.seq_lens = _int32_dense(seq_lens)
+        self.batch = int(self.seq_lens.numel())
+        if self.block_tables.size(0) != self.batch:
+            raise ValueError("block_tables and seq_lens disagree on the batch")
+        self.max_seq_len = int(max_seq_len)
+        self.n_kv_heads = int(n_kv_heads)
+        self.n_workgroups = int(n_workgroups)
+        dev = self.seq_lens.device
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            n = lib.aegkv_paged_decode_plan_size(self.batch, self.n_kv_heads, self.max_seq_len,
+                                                  self.n_workgroups)
+            if n < 0:
+                _lib.check(int(n), "decode_plan")
+            self.buffer = torch.empty(max(int(n), 1), dtype=torch.uint8, device=dev)
+            self.nbytes = int(n)
+            rc = lib.aegkv_paged_decode_plan(
+                self.block_tables.data_ptr(), self.block_tables.size(1), self.seq_lens.data_ptr(),
+                self.batch, self.max_seq_len, self.n_kv_heads, self.n_workgroups,
+                self.buffer.data_ptr(), self.nbytes, torch.cuda.current_stream(dev).cuda_stream)
+        _lib.check(rc, "decode_plan")
+
+
 def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
-                           block_tables: torch.Tensor, seq_lens: torch.Tensor, scale: float,
-                           max_seq_len: int, out: Optional[torch.Tensor] = None,
+                           block_tables: Optional[torch.Tensor], seq_lens: Optional[torch.Tensor],
+                           scale: float, max_seq_len: int, out: Optional[torch.Tensor] = None,
                            n_workgroups: int = 0,
-                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                           workspace: Optional[torch.Tensor] = None,
+                           plan: Optional[DecodePlan] = None) -> torch.Tensor:
     """Paged GQA decode attention: ``q [B, Hq, D]`` against per-layer cache
     views ``[N, 16, Hkv, D]``; returns ``out [B, Hq, D]`` in q's dtype.
     ``n_workgroups`` = 0 spreads the batch over one workgroup per CU; a
     positive count forces that many (same result).  ``workspace``: from
     :func:`attention_workspace` (reusable on one stream); by default a cached
-    one per (device, stream)."""
+    one per (device, stream).  ``plan``: a :class:`DecodePlan` of this step's
+    tables and lengths (then ``block_tables``/``seq_lens`` may be None, or
+    must be the tensors it was built from); the result is identical."""
+    if plan is not None:
+        for given, held, name in ((block_tables, plan.block_tables, "block_tables"),
+                                  (seq_lens, plan.seq_lens, "seq_lens")):
+            if given is not None and given.data_ptr() != held.data_ptr():
+                raise ValueError(f"{name} is not the tensor the plan was built from")
+        if (max_seq_len != plan.max_seq_len or n_workgroups != plan.n_workgroups
+                or q.size(0) != plan.batch or key_cache.size(2) != plan.n_kv_heads):
+            raise ValueError("the plan was built for another batch, max_seq_len, kv-head count "
+                             "or workgroup count")
+        block_tables, seq_lens = plan.block_tables, plan.seq_lens
     if q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.size(2) or not q.is_cuda:
         raise ValueError("q must be a GPU tensor [B, Hq, D] with dense heads")
     _check_cache_view(key_cache, "key_cache")
@@ -209,10 +262,8 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
         raise ValueError("q, key_cache and value_cache must share a bf16/fp16 dtype")
     B, Hq, D = q.shape
     N, bs, Hkv, _ = key_cache.shape
-    bt = block_tables if (block_tables.dtype == torch.int32 and block_tables.is_contiguous()) \
-        else block_tables.to(torch.int32).contiguous()
-    sl = seq_lens if (seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()) \
-        else seq_lens.to(torch.int32).contiguous()
+    bt = _int32_dense(block_tables)
+    sl = _int32_dense(seq_lens)
     if out is None:
         out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     elif out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D:
@@ -228,11 +279,18 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
                          f"the call needs {ws_bytes}")
     ws_ptr = workspace.data_ptr() if (workspace is not None and ws_bytes > 0) else None
     with torch.cuda.device(q.device):
-        rc = _lib.load().aegkv_paged_decode_attention(
-            out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), key_cache.data_ptr(),
-            value_cache.data_ptr(), key_cache.stride(0), N, bt.data_ptr(), bt.size(1),
-            sl.data_ptr(), B, max_seq_len, Hq, Hkv, D, bs, float(scale), _DTYPES[q.dtype],
-            n_workgroups, ws_ptr, ws_bytes if ws_ptr else 0, _stream(q))
+        if plan is not None:
+            rc = _lib.load().aegkv_paged_decode_attention_planned(
+                out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), key_cache.data_ptr(),
+                value_cache.data_ptr(), key_cache.stride(0), N, plan.buffer.data_ptr(),
+                plan.nbytes, sl.data_ptr(), B, max_seq_len, Hq, Hkv, D, bs, float(scale),
+                _DTYPES[q.dtype], n_workgroups, ws_ptr, ws_bytes if ws_ptr else 0, _stream(q))
+        else:
+            rc = _lib.load().aegkv_paged_decode_attention(
+                out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), key_cache.data_ptr(),
+                value_cache.data_ptr(), key_cache.stride(0), N, bt.data_ptr(), bt.size(1),
+                sl.data_ptr(), B, max_seq_len, Hq, Hkv, D, bs, float(scale), _DTYPES[q.dtype],
+                n_workgroups, ws_ptr, ws_bytes if ws_ptr else 0, _stream(q))
     _lib.check(rc, "paged_decode_attention")
     return out
 

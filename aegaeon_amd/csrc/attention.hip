@@ -159,7 +159,33 @@ struct AttnArgs {
   float2* part_ml;      // [slots][hpg] (running max in log2 units, sum)
   int32_t stage_slots;  // finished pieces a wave holds in LDS (0: stored at once)
   int32_t stage_off;    // byte offset of the staging area in dynamic LDS
+  // decode plan (planned launches only): workgroup records, first block ids
+  // of each workgroup's range, block ids in item order
+  const int32_t* plan_wg;
+  const int32_t* plan_first;
+  const int32_t* plan_ids;
 };
+
+// Decode plan, in one device buffer: per main-kernel workgroup a record of 8
+// int32 (first kv-head group or -1 for an idle workgroup, last group, first
+// item and its sequence, end item in the last group, the batch's first
+// non-empty sequence), the merge descriptors, the block ids of the first 64
+// items of each workgroup's range, then the block ids of all items in item
+// order (item i = block i - bcum[b] of the sequence b holding it).
+struct PlanLayout {
+  int64_t wg, desc, first, ids, total;
+};
+inline PlanLayout plan_layout(int64_t batch, int64_t n_wg, int64_t nblk_max) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  PlanLayout l;
+  l.wg = 0;
+  l.desc = up(n_wg * 32);
+  l.first = l.desc + up(n_wg * 16);
+  l.ids = l.first + up(n_wg * 64 * 4);
+  l.total = l.ids + up(batch * nblk_max * 4);
+  return l;
+}
+constexpr int kPlanRecord = 8;  // int32 per workgroup record
 
 // Workspace layout of one launch: the workgroups' descriptors, then the
 // partials of n_wg + n_groups * batch slots (a workgroup writes at most one
@@ -401,10 +427,16 @@ __device__ __forceinline__ void get_record(const uint8_t* rec, f32x4* acc, float
 // an L2 hit that is never computed).  Block ids come 64 items at a time, one
 // per lane, with the next 64 loaded a chunk ahead; an unreadable id loads
 // block 0 and is masked (the host guarantees n_blocks >= 1).
-template <int DT, int D, int NBUF>
+//
+// With a plan (PLANNED) the ids come from its item-order list, and `id_first`
+// holds the ids of items [i0, i0 + 64) when the caller loaded them (the
+// range's first pass), so no table lookup stands between the start and the
+// first K/V loads.
+template <int DT, int D, int NBUF, bool PLANNED>
 __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s_bcum,
                                              const int32_t* s_len, uint8_t* stage, int4* meta,
-                                             int grp, int b0, int i0, int i1) {
+                                             int grp, int b0, int i0, int i1, bool have_first,
+                                             int id_first) {
   constexpr int KS = D / 32;
   constexpr int DPL = D / 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -431,11 +463,15 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   // checked before a search)
   auto item_id = [&](int i, int bh) -> int {
     i = min(i, i1 - 1);
-    int b = bh;
-    if (s_bcum[b + 1] <= i) b = s_bcum[b + 2] > i ? b + 1 : seq_at(s_bcum, a.batch, i);
-    return a.block_tables[(int64_t)b * a.max_blocks + (i - s_bcum[b])];
+    if constexpr (PLANNED) {
+      return a.plan_ids[i];
+    } else {
+      int b = bh;
+      if (s_bcum[b + 1] <= i) b = s_bcum[b + 2] > i ? b + 1 : seq_at(s_bcum, a.batch, i);
+      return a.block_tables[(int64_t)b * a.max_blocks + (i - s_bcum[b])];
+    }
   };
-  int id_cur = item_id(i0 + lane, bc);       // items [cbase, cbase + 64)
+  int id_cur = PLANNED && have_first ? id_first : item_id(i0 + lane, bc);  // [cbase, cbase + 64)
   int id_nxt = item_id(i0 + 64 + lane, bc);  // items [cbase + 64, cbase + 128)
   int cbase = i0;
   // id of item i >= cbase (uniform): rotates the chunks when i leaves the
@@ -555,52 +591,28 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   flush();
 }
 
-// Workgroup that holds position P of the flattened range (the largest w with
-// floor(w * total / n_act) <= P; n_act <= total, so every range is non-empty).
-// floor(num / den) for 0 <= num, den < 2^52 (the host bounds every operand
-// below by that): the correctly rounded double quotient is within one of the
-// exact one, and one integer step corrects it.  A fraction of the cost of a
-// 64-bit integer division, which the startup of every workgroup needs several
-// of.
-__device__ __forceinline__ int64_t div_floor(int64_t num, int64_t den) {
-  int64_t q = (int64_t)((double)num / (double)den);
-  if (q * den > num) --q;
-  else if ((q + 1) * den <= num) ++q;
-  return q;
-}
-
-__device__ __forceinline__ int64_t owner_of(int64_t P, int64_t total, int64_t n_act) {
-  return div_floor((P + 1) * n_act - 1, total);
-}
-
-template <int DT, int D, int NBUF>
-__global__ __launch_bounds__(64 * kHeadsPerGroup, D >= 256 ? 1 : 2) void
-paged_decode_attention_kernel(AttnArgs a) {
-  // cum[batch + 1] (positions), len[batch], bcum[batch + 1] (blocks)
-  extern __shared__ int32_t s_mem[];
-  __shared__ int32_t s_wave_tot[2][kHeadsPerGroup];
-  __shared__ int32_t s_find[2];
-  __shared__ int4 s_meta[kHeadsPerGroup][kMaxStage];
-  int32_t* s_cum = s_mem;
-  int32_t* s_len = s_mem + a.batch + 1;
-  int32_t* s_bcum = s_len + a.batch;
+// Prefix sums of the batch's positions and blocks (lengths clamped to
+// max_seq_len) into LDS: s_cum[batch + 1] (cost units), s_bcum[batch + 1]
+// (blocks), s_len[batch].  Every thread of the 64 * kHeadsPerGroup takes part.
+__device__ __forceinline__ void scan_batch(const int32_t* seq_lens, int batch, int max_seq_len,
+                                           int32_t* s_cum, int32_t* s_bcum, int32_t* s_len,
+                                           int32_t (*s_wave_tot)[kHeadsPerGroup]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-
   // Prefix sums of the batch's positions and blocks: thread t owns sequences
   // [t * per, t * per + per); a wave scan plus the wave totals give each
   // thread its exclusive offsets.
   {
-    const int per = (a.batch + 64 * kHeadsPerGroup - 1) / (64 * kHeadsPerGroup);
+    const int per = (batch + 64 * kHeadsPerGroup - 1) / (64 * kHeadsPerGroup);
     const int b0 = tid * per;
     int lens[kScanPerThread];
     int cnt = 0, bcnt = 0;
     // all loads issued before any is used (clamped index, masked after)
 #pragma unroll
-    for (int k = 0; k < kScanPerThread; ++k) lens[k] = a.seq_lens[min(b0 + k, a.batch - 1)];
+    for (int k = 0; k < kScanPerThread; ++k) lens[k] = seq_lens[min(b0 + k, batch - 1)];
 #pragma unroll
     for (int k = 0; k < kScanPerThread; ++k) {
-      lens[k] = (k < per && b0 + k < a.batch) ? min(max(lens[k], 0), a.max_seq_len) : 0;
+      lens[k] = (k < per && b0 + k < batch) ? min(max(lens[k], 0), max_seq_len) : 0;
       cnt += cost_units(lens[k]);
       bcnt += (lens[k] + kBlockSize - 1) / kBlockSize;
     }
@@ -626,7 +638,7 @@ paged_decode_attention_kernel(AttnArgs a) {
     int excl = base + x - cnt, bexcl = bbase + y - bcnt;
 #pragma unroll
     for (int k = 0; k < kScanPerThread; ++k) {
-      if (k < per && b0 + k < a.batch) {
+      if (k < per && b0 + k < batch) {
         s_cum[b0 + k] = excl;
         s_bcum[b0 + k] = bexcl;
         s_len[b0 + k] = lens[k];
@@ -635,11 +647,55 @@ paged_decode_attention_kernel(AttnArgs a) {
       }
     }
     if (tid == 64 * kHeadsPerGroup - 1) {
-      s_cum[a.batch] = base + x;
-      s_bcum[a.batch] = bbase + y;
+      s_cum[batch] = base + x;
+      s_bcum[batch] = bbase + y;
     }
     __syncthreads();
   }
+}
+
+// Workgroup that holds position P of the flattened range (the largest w with
+// floor(w * total / n_act) <= P; n_act <= total, so every range is non-empty).
+// floor(num / den) for 0 <= num, den < 2^52 (the host bounds every operand
+// below by that): the correctly rounded double quotient is within one of the
+// exact one, and one integer step corrects it.  A fraction of the cost of a
+// 64-bit integer division, which the startup of every workgroup needs several
+// of.
+__device__ __forceinline__ int64_t div_floor(int64_t num, int64_t den) {
+  int64_t q = (int64_t)((double)num / (double)den);
+  if (q * den > num) --q;
+  else if ((q + 1) * den <= num) ++q;
+  return q;
+}
+
+__device__ __forceinline__ int64_t owner_of(int64_t P, int64_t total, int64_t n_act) {
+  return div_floor((P + 1) * n_act - 1, total);
+}
+
+template <int DT, int D, int NBUF, bool PLANNED>
+__global__ __launch_bounds__(64 * kHeadsPerGroup, D >= 256 ? 1 : 2) void
+paged_decode_attention_kernel(AttnArgs a) {
+  // cum[batch + 1] (positions), len[batch], bcum[batch + 1] (blocks)
+  extern __shared__ int32_t s_mem[];
+  __shared__ int32_t s_wave_tot[2][kHeadsPerGroup];
+  __shared__ int32_t s_find[2];
+  __shared__ int4 s_meta[kHeadsPerGroup][kMaxStage];
+  int32_t* s_cum = s_mem;
+  int32_t* s_len = s_mem + a.batch + 1;
+  int32_t* s_bcum = s_len + a.batch;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+
+  // A planned workgroup's record and the block ids of its first 64 items,
+  // loaded before the scan so that they arrive while it runs.
+  int rec[kPlanRecord] = {};
+  int id_first = 0;
+  if constexpr (PLANNED) {
+#pragma unroll
+    for (int k = 0; k < kPlanRecord; ++k) rec[k] = a.plan_wg[(int64_t)blockIdx.x * kPlanRecord + k];
+    id_first = a.plan_first[(int64_t)blockIdx.x * 64 + lane];
+  }
+  scan_batch(a.seq_lens, a.batch, a.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot);
   // Empty sequences have no positions: workgroup b % n_wg writes their zeros.
   for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
     if (s_cum[b + 1] != s_cum[b]) continue;  // uniform over the workgroup
@@ -648,6 +704,22 @@ paged_decode_attention_kernel(AttnArgs a) {
       *reinterpret_cast<u32x4*>(op + e) = u32x4{0u, 0u, 0u, 0u};
   }
 
+  uint8_t* stage = reinterpret_cast<uint8_t*>(s_mem) + a.stage_off +
+                   wave * a.stage_slots * a.group * 4 * stage_record_bytes<D>();
+  if constexpr (PLANNED) {
+    if (uni(rec[0]) < 0) return;  // idle workgroup
+    const int items = s_bcum[a.batch];
+    for (int grp = uni(rec[0]); grp <= uni(rec[1]); ++grp) {
+      const bool first_pass = grp == uni(rec[0]);
+      const int i0 = first_pass ? uni(rec[2]) : 0;
+      const int b0 = first_pass ? uni(rec[3]) : uni(rec[5]);
+      const int i1 = grp == uni(rec[1]) ? uni(rec[4]) : items;
+      if (i1 > i0)
+        attend_items<DT, D, NBUF, true>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0, i0, i1,
+                                        first_pass, id_first);
+    }
+    return;
+  }
   const int64_t W = s_cum[a.batch];
   const int64_t total = W * a.n_groups;
   // With fewer positions than workgroups only the first `total` take part, so
@@ -662,8 +734,6 @@ paged_decode_attention_kernel(AttnArgs a) {
   // Every value below is uniform over the workgroup.  A sequence occupies
   // positions [s_cum[b], s_cum[b + 1]) of its group: kSegmentCost charge
   // positions, then one per block.
-  uint8_t* stage = reinterpret_cast<uint8_t*>(s_mem) + a.stage_off +
-                   wave * a.stage_slots * a.group * 4 * stage_record_bytes<D>();
   bool first_pass = true;
   while (P < p_end) {  // one pass per kv-head group the range touches
     const int grp = (int)div_floor(P, W);
@@ -697,10 +767,103 @@ paged_decode_attention_kernel(AttnArgs a) {
                                  : make_int4(-1, 0, 0, 0);
       first_pass = false;
     }
-    if (i1 > i0) attend_items<DT, D, NBUF>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0, i0, i1);
+    if (i1 > i0)
+      attend_items<DT, D, NBUF, false>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0, i0, i1,
+                                       false, 0);
     P = q_end;
     __syncthreads();  // s_find is rewritten by the next pass
   }
+}
+
+struct PlanArgs {
+  const int32_t* block_tables;
+  int32_t max_blocks;
+  const int32_t* seq_lens;
+  int32_t batch;
+  int32_t max_seq_len;
+  int32_t n_groups;
+  int32_t n_wg;
+  int32_t* wg;
+  int4* desc;
+  int32_t* first;
+  int32_t* ids;
+};
+
+// Builds a decode plan (see PlanLayout) with the partition the attention
+// kernel computes for itself: every workgroup scans the lengths, then the
+// grid shares the per-workgroup records, the first-64 id lists and the
+// item-order ids.
+__global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanArgs p) {
+  extern __shared__ int32_t s_mem[];
+  __shared__ int32_t s_wave_tot[2][kHeadsPerGroup];
+  int32_t* s_cum = s_mem;
+  int32_t* s_len = s_mem + p.batch + 1;
+  int32_t* s_bcum = s_len + p.batch;
+  scan_batch(p.seq_lens, p.batch, p.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot);
+  const int64_t W = s_cum[p.batch];
+  const int items = s_bcum[p.batch];
+  const int64_t total = W * p.n_groups;
+  const int64_t n_act = min((int64_t)p.n_wg, total);
+  const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
+  const int gsz = gridDim.x * blockDim.x;
+  auto items_before = [&](int b, int pos) -> int {
+    const int nblk = s_bcum[b + 1] - s_bcum[b];
+    return s_bcum[b] + min(max(pos - s_cum[b] - kSegmentCost, 0), nblk);
+  };
+  // workgroup w's range: first and last kv-head group, first item and its
+  // sequence, end item in the last group and in the first
+  struct Range {
+    int gf, gl, i0, b0, i1l, i1f;
+  };
+  auto range_of = [&](int w) -> Range {
+    const int64_t P = div_floor((int64_t)w * total, n_act);
+    const int64_t pe = div_floor((int64_t)(w + 1) * total, n_act);
+    Range r;
+    r.gf = (int)div_floor(P, W);
+    r.gl = (int)div_floor(pe - 1, W);
+    const int p0 = (int)(P - (int64_t)r.gf * W);
+    r.b0 = seq_at(s_cum, p.batch, p0);
+    r.i0 = items_before(r.b0, p0);
+    const int pl = (int)(pe - (int64_t)r.gl * W);
+    r.i1l = pl == (int)W ? items : items_before(seq_at(s_cum, p.batch, pl), pl);
+    r.i1f = r.gf == r.gl ? r.i1l : items;
+    return r;
+  };
+  for (int w = gtid; w < p.n_wg; w += gsz) {
+    int32_t* rec = p.wg + (int64_t)w * kPlanRecord;
+    if (w >= n_act) {
+      rec[0] = -1;
+      p.desc[w] = make_int4(-1, 0, 0, 0);
+      continue;
+    }
+    const Range r = range_of(w);
+    rec[0] = r.gf;
+    rec[1] = r.gl;
+    rec[2] = r.i0;
+    rec[3] = r.b0;
+    rec[4] = r.i1l;
+    rec[5] = seq_at(s_cum, p.batch, 0);  // first non-empty sequence
+    rec[6] = 0;
+    rec[7] = 0;
+    // the range's first piece is the only one that can end a cut sequence
+    const int64_t pbase = (int64_t)r.gf * W;
+    const int64_t w0 = owner_of(pbase + s_cum[r.b0] + kSegmentCost, total, n_act);
+    const int64_t w1 = owner_of(pbase + s_cum[r.b0 + 1] - 1, total, n_act);
+    p.desc[w] = (w0 != w1 && w1 == (int64_t)w) ? make_int4(r.b0, r.gf, (int)w0, (int)(w1 - w0 + 1))
+                                               : make_int4(-1, 0, 0, 0);
+  }
+  auto id_of = [&](int i) -> int32_t {
+    const int b = seq_at(s_bcum, p.batch, i);
+    return p.block_tables[(int64_t)b * p.max_blocks + (i - s_bcum[b])];
+  };
+  for (int64_t e = gtid; e < (int64_t)p.n_wg * 64; e += gsz) {
+    const int w = (int)(e >> 6);
+    if (w >= n_act) continue;
+    const Range r = range_of(w);
+    if (r.i1f <= r.i0) continue;  // the first pass holds no block
+    p.first[e] = id_of(min(r.i0 + (int)(e & 63), r.i1f - 1));
+  }
+  for (int i = gtid; i < items; i += gsz) p.ids[i] = id_of(i);
 }
 
 // Merge the pieces of the cut sequence whose last block workgroup
@@ -849,8 +1012,12 @@ int launch_combine(const AttnArgs& a, hipStream_t stream) {
 
 template <int DT, int D>
 int launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>()>), dim3(a.n_wg),
-                     dim3(64 * kHeadsPerGroup), lds, stream, a);
+  if (a.plan_wg)
+    hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>(), true>),
+                       dim3(a.n_wg), dim3(64 * kHeadsPerGroup), lds, stream, a);
+  else
+    hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>(), false>),
+                       dim3(a.n_wg), dim3(64 * kHeadsPerGroup), lds, stream, a);
   AEGKV_HIP_TRY(hipGetLastError());
   const int items = a.group * (D / 4);  // <= 16 * D / 4
   if (items <= 64) return launch_combine<DT, D, 1>(a, stream);
@@ -863,42 +1030,17 @@ int launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
 }  // namespace
 }  // namespace aegkv
 
-using namespace aegkv;
-
-extern "C" {
-
-int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_heads,
-                                                     int32_t n_kv_heads, int32_t head_dim,
-                                                     int32_t max_seq_len, int32_t dtype,
-                                                     int32_t n_workgroups) {
-  if (batch < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads ||
-      n_workgroups < 0 || max_seq_len < 0)
-    return AEGKV_ERR_INVALID_ARG;
-  if (n_workgroups > kMaxWorkgroups) return AEGKV_ERR_UNSUPPORTED;
-  if ((head_dim != 64 && head_dim != 128 && head_dim != 256) ||
-      (dtype != AEGKV_DTYPE_BF16 && dtype != AEGKV_DTYPE_FP16) || n_q_heads / n_kv_heads > 16)
-    return AEGKV_ERR_UNSUPPORTED;
-  if (batch == 0) return 0;
-  const int32_t chunk = std::min(batch, kMaxBatch);
-  int n_wg = 0;
-  const int rc = workgroups_for(n_workgroups, &n_wg);
-  if (rc) return rc > 0 ? AEGKV_ERR_RUNTIME : rc;
-  const int32_t group = n_q_heads / n_kv_heads;
-  const int32_t n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
-  if (!positions_fit(chunk, ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize, n_groups, n_wg))
-    return AEGKV_ERR_UNSUPPORTED;
-  return workspace_layout(chunk, kHeadsPerGroup * group, head_dim, n_wg, n_groups).total;
-}
-
-int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void* q,
-                                 int64_t q_batch_stride, const void* key_cache,
-                                 const void* value_cache, int64_t cache_block_stride,
-                                 int64_t n_blocks, const int32_t* block_tables,
-                                 int32_t max_blocks, const int32_t* seq_lens, int32_t batch,
-                                 int32_t max_seq_len, int32_t n_q_heads, int32_t n_kv_heads,
-                                 int32_t head_dim, int32_t block_size, float scale,
-                                 int32_t dtype, int32_t n_workgroups, void* workspace,
-                                 uint64_t workspace_bytes, aegkv_stream_t stream) {
+namespace aegkv {
+namespace {
+// Both entry points: `plan` (with plan_bytes) replaces the block tables when
+// given.
+int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride,
+                  const void* key_cache, const void* value_cache, int64_t cache_block_stride,
+                  int64_t n_blocks, const int32_t* block_tables, int32_t max_blocks,
+                  const void* plan, uint64_t plan_bytes, const int32_t* seq_lens, int32_t batch,
+                  int32_t max_seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                  int32_t block_size, float scale, int32_t dtype, int32_t n_workgroups,
+                  void* workspace, uint64_t workspace_bytes, aegkv_stream_t stream) {
   if (batch < 0 || max_seq_len < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_blocks < 0 ||
       n_blocks < 0 || n_workgroups < 0)
     return AEGKV_ERR_INVALID_ARG;
@@ -907,15 +1049,17 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
       n_q_heads / n_kv_heads > 16 || (dtype != AEGKV_DTYPE_BF16 && dtype != AEGKV_DTYPE_FP16))
     return AEGKV_ERR_UNSUPPORTED;
   if (batch == 0) return AEGKV_OK;
-  if (!out || !q || !key_cache || !value_cache || !block_tables || !seq_lens || n_blocks == 0)
+  if (!out || !q || !key_cache || !value_cache || (!block_tables && !plan) || !seq_lens ||
+      n_blocks == 0)
     return AEGKV_ERR_INVALID_ARG;
+  if (plan && batch > kMaxBatch) return AEGKV_ERR_UNSUPPORTED;
   if (!aligned16(out) || !aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache) ||
       ((q_batch_stride * 2) & 15) || ((out_batch_stride * 2) & 15) ||
       ((cache_block_stride * 2) & 15))
     return AEGKV_ERR_MISALIGNED;
   if (n_q_heads > 65535 || n_workgroups > kMaxWorkgroups) return AEGKV_ERR_UNSUPPORTED;
   const int64_t nblk_max = ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize;
-  if (nblk_max > max_blocks) return AEGKV_ERR_INVALID_ARG;
+  if (!plan && nblk_max > max_blocks) return AEGKV_ERR_INVALID_ARG;
   const int32_t chunk = std::min(batch, kMaxBatch);
   int n_wg = 0;
   int rc = workgroups_for(n_workgroups, &n_wg);
@@ -946,6 +1090,17 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
   a.q_bstride = q_batch_stride;
   a.out_bstride = out_batch_stride;
   a.desc = reinterpret_cast<int4*>(ws);
+  a.plan_wg = a.plan_first = a.plan_ids = nullptr;
+  if (plan) {
+    const PlanLayout pl = plan_layout(batch, n_wg, nblk_max);
+    if (plan_bytes < (uint64_t)pl.total) return AEGKV_ERR_INVALID_ARG;
+    if (!aligned16(plan)) return AEGKV_ERR_MISALIGNED;
+    const uint8_t* pb = static_cast<const uint8_t*>(plan);
+    a.plan_wg = reinterpret_cast<const int32_t*>(pb + pl.wg);
+    a.desc = reinterpret_cast<int4*>(const_cast<uint8_t*>(pb + pl.desc));
+    a.plan_first = reinterpret_cast<const int32_t*>(pb + pl.first);
+    a.plan_ids = reinterpret_cast<const int32_t*>(pb + pl.ids);
+  }
   a.part_ml = reinterpret_cast<float2*>(ws + lay.desc_bytes);
   a.part_o = reinterpret_cast<float*>(ws + lay.desc_bytes + lay.ml_bytes);
   hipStream_t st = (hipStream_t)stream;
@@ -959,7 +1114,7 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
     a.batch = std::min(kMaxBatch, batch - c);
     a.q = static_cast<const uint16_t*>(q) + (int64_t)c * q_batch_stride;
     a.out = static_cast<uint16_t*>(out) + (int64_t)c * out_batch_stride;
-    a.block_tables = block_tables + (int64_t)c * max_blocks;
+    a.block_tables = block_tables ? block_tables + (int64_t)c * max_blocks : nullptr;
     a.seq_lens = seq_lens + c;
     const size_t lds = lds_bytes(a, ds->max_lds);
     switch (head_dim) {
@@ -973,6 +1128,122 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
     if (rc) return rc;
   }
   return AEGKV_OK;
+}
+}  // namespace
+}  // namespace aegkv
+
+using namespace aegkv;
+
+extern "C" {
+
+int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_heads,
+                                                     int32_t n_kv_heads, int32_t head_dim,
+                                                     int32_t max_seq_len, int32_t dtype,
+                                                     int32_t n_workgroups) {
+  if (batch < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads ||
+      n_workgroups < 0 || max_seq_len < 0)
+    return AEGKV_ERR_INVALID_ARG;
+  if (n_workgroups > kMaxWorkgroups) return AEGKV_ERR_UNSUPPORTED;
+  if ((head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+      (dtype != AEGKV_DTYPE_BF16 && dtype != AEGKV_DTYPE_FP16) || n_q_heads / n_kv_heads > 16)
+    return AEGKV_ERR_UNSUPPORTED;
+  if (batch == 0) return 0;
+  const int32_t chunk = std::min(batch, kMaxBatch);
+  int n_wg = 0;
+  const int rc = workgroups_for(n_workgroups, &n_wg);
+  if (rc) return rc > 0 ? AEGKV_ERR_RUNTIME : rc;
+  const int32_t group = n_q_heads / n_kv_heads;
+  const int32_t n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  if (!positions_fit(chunk, ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize, n_groups, n_wg))
+    return AEGKV_ERR_UNSUPPORTED;
+  return workspace_layout(chunk, kHeadsPerGroup * group, head_dim, n_wg, n_groups).total;
+}
+
+
+int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void* q,
+                                 int64_t q_batch_stride, const void* key_cache,
+                                 const void* value_cache, int64_t cache_block_stride,
+                                 int64_t n_blocks, const int32_t* block_tables,
+                                 int32_t max_blocks, const int32_t* seq_lens, int32_t batch,
+                                 int32_t max_seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, int32_t block_size, float scale,
+                                 int32_t dtype, int32_t n_workgroups, void* workspace,
+                                 uint64_t workspace_bytes, aegkv_stream_t stream) {
+  if (batch > 0 && !block_tables) return AEGKV_ERR_INVALID_ARG;
+  return run_attention(out, out_batch_stride, q, q_batch_stride, key_cache, value_cache,
+                       cache_block_stride, n_blocks, block_tables, max_blocks, nullptr, 0,
+                       seq_lens, batch, max_seq_len, n_q_heads, n_kv_heads, head_dim,
+                       block_size, scale, dtype, n_workgroups, workspace, workspace_bytes,
+                       stream);
+}
+
+int64_t aegkv_paged_decode_plan_size(int32_t batch, int32_t n_kv_heads, int32_t max_seq_len,
+                                     int32_t n_workgroups) {
+  if (batch < 0 || n_kv_heads <= 0 || max_seq_len < 0 || n_workgroups < 0)
+    return AEGKV_ERR_INVALID_ARG;
+  if (batch > kMaxBatch || n_workgroups > kMaxWorkgroups) return AEGKV_ERR_UNSUPPORTED;
+  if (batch == 0) return 0;
+  int n_wg = 0;
+  const int rc = workgroups_for(n_workgroups, &n_wg);
+  if (rc) return rc > 0 ? AEGKV_ERR_RUNTIME : rc;
+  const int64_t nblk_max = ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize;
+  const int32_t n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  if (!positions_fit(batch, nblk_max, n_groups, n_wg)) return AEGKV_ERR_UNSUPPORTED;
+  return plan_layout(batch, n_wg, nblk_max).total;
+}
+
+int aegkv_paged_decode_plan(const int32_t* block_tables, int32_t max_blocks,
+                            const int32_t* seq_lens, int32_t batch, int32_t max_seq_len,
+                            int32_t n_kv_heads, int32_t n_workgroups, void* plan,
+                            uint64_t plan_bytes, aegkv_stream_t stream) {
+  const int64_t need = aegkv_paged_decode_plan_size(batch, n_kv_heads, max_seq_len, n_workgroups);
+  if (need < 0) return (int)need;
+  if (batch == 0) return AEGKV_OK;
+  if (!block_tables || !seq_lens || !plan || max_blocks < 0) return AEGKV_ERR_INVALID_ARG;
+  const int64_t nblk_max = ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize;
+  if (nblk_max > max_blocks) return AEGKV_ERR_INVALID_ARG;
+  if (plan_bytes < (uint64_t)need) return AEGKV_ERR_INVALID_ARG;
+  if (!aligned16(plan)) return AEGKV_ERR_MISALIGNED;
+  int n_wg = 0;
+  int rc = workgroups_for(n_workgroups, &n_wg);
+  if (rc) return rc;
+  const PlanLayout pl = plan_layout(batch, n_wg, nblk_max);
+  uint8_t* pb = static_cast<uint8_t*>(plan);
+  PlanArgs p;
+  p.block_tables = block_tables;
+  p.max_blocks = max_blocks;
+  p.seq_lens = seq_lens;
+  p.batch = batch;
+  p.max_seq_len = max_seq_len;
+  p.n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  p.n_wg = n_wg;
+  p.wg = reinterpret_cast<int32_t*>(pb + pl.wg);
+  p.desc = reinterpret_cast<int4*>(pb + pl.desc);
+  p.first = reinterpret_cast<int32_t*>(pb + pl.first);
+  p.ids = reinterpret_cast<int32_t*>(pb + pl.ids);
+  const int64_t work = std::max<int64_t>((int64_t)n_wg * 64, (int64_t)batch * nblk_max);
+  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(1024, (work + 255) / 256));
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(grid), dim3(64 * kHeadsPerGroup),
+                     (size_t)(3 * batch + 2) * sizeof(int32_t), (hipStream_t)stream, p);
+  AEGKV_HIP_TRY(hipGetLastError());
+  return AEGKV_OK;
+}
+
+int aegkv_paged_decode_attention_planned(void* out, int64_t out_batch_stride, const void* q,
+                                         int64_t q_batch_stride, const void* key_cache,
+                                         const void* value_cache, int64_t cache_block_stride,
+                                         int64_t n_blocks, const void* plan, uint64_t plan_bytes,
+                                         const int32_t* seq_lens, int32_t batch,
+                                         int32_t max_seq_len, int32_t n_q_heads,
+                                         int32_t n_kv_heads, int32_t head_dim,
+                                         int32_t block_size, float scale, int32_t dtype,
+                                         int32_t n_workgroups, void* workspace,
+                                         uint64_t workspace_bytes, aegkv_stream_t stream) {
+  if (batch > 0 && !plan) return AEGKV_ERR_INVALID_ARG;
+  return run_attention(out, out_batch_stride, q, q_batch_stride, key_cache, value_cache,
+                       cache_block_stride, n_blocks, nullptr, 0, plan, plan_bytes, seq_lens,
+                       batch, max_seq_len, n_q_heads, n_kv_heads, head_dim, block_size, scale,
+                       dtype, n_workgroups, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -198,6 +198,40 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
                                  int32_t n_workgroups, void* workspace,
                                  uint64_t workspace_bytes, aegkv_stream_t stream);
 
+/* Decode plan: the work split of aegkv_paged_decode_attention for one batch
+ * of block tables and lengths, built once per decode step and shared by every
+ * layer's call (the layers of a step attend over the same tables, as the
+ * reference's attention metadata is built once per step at
+ * aegaeon/aegaeon/worker.py:694-711 and used by every layer of the forward).
+ * It has no counterpart in the reference's call: it moves the per-call
+ * partition and block-table lookups out of each layer's critical path.
+ *   aegkv_paged_decode_plan_size: DEVICE bytes of the plan (negative status
+ *     when unsupported: batch above 2048, or the limits of the attention).
+ *   aegkv_paged_decode_plan: writes the plan from DEVICE block_tables and
+ *     seq_lens (asynchronous on `stream`).  The tables and lengths must not
+ *     change while the plan is in use.
+ *   aegkv_paged_decode_attention_planned: the attention of
+ *     aegkv_paged_decode_attention (same arguments and workspace) with the
+ *     plan in place of the block tables; batch, max_seq_len, n_kv_heads,
+ *     n_workgroups and seq_lens must be the ones the plan was built with.
+ *     Results are identical to the unplanned call, bit for bit. */
+int64_t aegkv_paged_decode_plan_size(int32_t batch, int32_t n_kv_heads, int32_t max_seq_len,
+                                     int32_t n_workgroups);
+int aegkv_paged_decode_plan(const int32_t* block_tables, int32_t max_blocks,
+                            const int32_t* seq_lens, int32_t batch, int32_t max_seq_len,
+                            int32_t n_kv_heads, int32_t n_workgroups, void* plan,
+                            uint64_t plan_bytes, aegkv_stream_t stream);
+int aegkv_paged_decode_attention_planned(void* out, int64_t out_batch_stride, const void* q,
+                                         int64_t q_batch_stride, const void* key_cache,
+                                         const void* value_cache, int64_t cache_block_stride,
+                                         int64_t n_blocks, const void* plan, uint64_t plan_bytes,
+                                         const int32_t* seq_lens, int32_t batch,
+                                         int32_t max_seq_len, int32_t n_q_heads,
+                                         int32_t n_kv_heads, int32_t head_dim,
+                                         int32_t block_size, float scale, int32_t dtype,
+                                         int32_t n_workgroups, void* workspace,
+                                         uint64_t workspace_bytes, aegkv_stream_t stream);
+
 /* ---- a4: decode/prefill input preparation --------------------------------
  * Replaces the host loops of Worker._prepare_model_inputs
  * (aegaeon/aegaeon/worker.py:596-676) and make_tensor_with_pad

@@ -159,6 +159,40 @@ def test_attention_argument_checks_and_workspace_size(lib):
     assert attn(q=mis) == MISALIGNED
 
 
+def test_decode_plan_host_checks(lib):
+    """Plan sizing and the host checks of plan building and planned calls
+    (explicit workgroup counts: no device query, no launch)."""
+    raw, p = _buf(1 << 20)
+    size = lib.aegkv_paged_decode_plan_size
+    up = lambda x: -(-x // 256) * 256  # noqa: E731
+    # (batch, Hkv, max_seq_len, n_workgroups): records of 8 int32, descriptors,
+    # 64 first ids per workgroup, then batch * ceil(max_seq_len / 16) ids
+    assert size(0, 4, 4096, 8) == 0
+    assert size(3, 4, 100, 8) == up(8 * 32) + up(8 * 16) + up(8 * 256) + up(3 * 7 * 4)
+    assert size(2049, 4, 100, 8) == UNSUP  # one launch's batch at most
+    assert size(3, 0, 100, 8) == INVALID
+    assert size(3, 4, -1, 8) == INVALID
+    assert size(3, 4, 100, 8193) == UNSUP
+    plan = lib.aegkv_paged_decode_plan
+    # (tables, max_blocks, seq_lens, batch, max_seq_len, Hkv, nwg, plan, plan_bytes, stream)
+    need = size(3, 4, 100, 8)
+    assert plan(p, 7, p, 3, 100, 4, 8, p, need - 1, None) == INVALID
+    assert plan(p, 6, p, 3, 100, 4, 8, p, need, None) == INVALID  # tables narrower than 100 tokens
+    assert plan(None, 7, p, 3, 100, 4, 8, p, need, None) == INVALID
+    raw2, mis = _buf(need + 64, misalign=4)
+    assert plan(p, 7, p, 3, 100, 4, 8, mis, need, None) == MISALIGNED
+    assert plan(p, 7, p, 0, 100, 4, 8, None, 0, None) == 0  # empty batch: nothing to do
+
+    def planned(batch=2, plan_ptr=p, plan_bytes=1 << 16, max_len=64):
+        return lib.aegkv_paged_decode_attention_planned(
+            p, 28 * 128, p, 28 * 128, p, p, 16 * 4 * 128, 8, plan_ptr, plan_bytes, p, batch,
+            max_len, 28, 4, 128, 16, 0.1, 0, 8, p, 1 << 20, None)
+
+    assert planned(plan_ptr=None) == INVALID
+    assert planned(plan_bytes=size(2, 4, 64, 8) - 1) == INVALID
+    assert planned(batch=2049, max_len=16) == UNSUP
+
+
 def test_prepare_inputs_host_checks(lib):
     """Argument errors are found on the host, before any device work."""
     raw, p = _buf(1 << 12)

@@ -232,3 +232,93 @@ def test_workspace_reused_across_calls(device):
         ref = ko.paged_decode_attention(ko.bits_to_float(q, "bf16"), ko.bits_to_float(kc, "bf16"),
                                         ko.bits_to_float(vc, "bf16"), padded, lens, scale)
         _check(to_bits(out), ref, "bf16")
+
+
+def _device_case(device, lens, Hq, Hkv, D, dtype, seed, pad_to=None):
+    rng = np.random.default_rng(seed)
+    lens, tables, padded, q, kc, vc = _setup(rng, lens, Hq, Hkv, D, dtype, pad_to=pad_to)
+    return (lens, padded, q, kc, vc, to_device_bits(q, dtype, device),
+            to_device_bits(kc, dtype, device), to_device_bits(vc, dtype, device),
+            torch.from_numpy(padded).to(device),
+            torch.from_numpy(lens.astype(np.int32)).to(device))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("Hq,Hkv,D", [(28, 4, 128), (16, 1, 64), (6, 2, 256), (12, 6, 128),
+                                      (40, 40, 128)])
+@pytest.mark.parametrize("nwg", [0, 1, 3, 64, 1000])
+def test_planned_call_is_bit_identical(device, dtype, Hq, Hkv, D, nwg):
+    """A decode plan reproduces the split the kernel computes for itself (the
+    same pieces, merged the same way): the planned call's output equals the
+    unplanned one bit for bit, for every workgroup count (one workgroup over
+    all sequences and all kv-head groups; more workgroups than blocks)."""
+    lens = [1, 15, 16, 17, 31, 64, 200, 517, 0, 1100]
+    _, _, _, _, _, q, kc, vc, bt, sl = _device_case(device, lens, Hq, Hkv, D, dtype, nwg + D)
+    scale = 1.0 / math.sqrt(D)
+    ref = A.paged_decode_attention(q, kc, vc, bt, sl, scale, 1100, n_workgroups=nwg)
+    plan = A.DecodePlan(bt, sl, 1100, Hkv, nwg)
+    got = A.paged_decode_attention(q, kc, vc, None, None, scale, 1100, n_workgroups=nwg,
+                                   plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
+def test_plan_serves_every_layer(device):
+    """One plan per step, many layers: each layer's queries and caches differ,
+    the tables and lengths do not.  Every planned output equals the unplanned
+    call and the float64 oracle."""
+    rng = np.random.default_rng(31)
+    lens = rng.integers(1, 3000, size=40)
+    lens[[3, 17]] = 0
+    lens, tables, padded, _, _, _ = _setup(rng, lens, 28, 4, 128, "bf16")
+    bt = torch.from_numpy(padded).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    ml = int(lens.max())
+    plan = A.DecodePlan(bt, sl, ml, 4)
+    scale = 1.0 / math.sqrt(128)
+    N = max(8, 2 * int(sum(-(-int(x) // 16) for x in lens)) + 3)
+    for layer in range(3):
+        q = random_bits(rng, (40, 28, 128), "bf16")
+        kc = random_bits(rng, (N, 16, 4, 128), "bf16")
+        vc = random_bits(rng, (N, 16, 4, 128), "bf16")
+        qd, kd, vd = (to_device_bits(x, "bf16", device) for x in (q, kc, vc))
+        got = A.paged_decode_attention(qd, kd, vd, bt, sl, scale, ml, plan=plan)
+        ref = A.paged_decode_attention(qd, kd, vd, bt, sl, scale, ml)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), layer
+        oracle = ko.paged_decode_attention(ko.bits_to_float(q, "bf16"), ko.bits_to_float(kc, "bf16"),
+                                           ko.bits_to_float(vc, "bf16"), padded, lens, scale)
+        _check(to_bits(got), oracle, "bf16")
+
+
+def test_plan_qwen_full_batch(device):
+    """The Qwen2.5-7B decode batch through a plan, against the unplanned call."""
+    wb = qwen_attention_batch(0)
+    g = wb.geometry
+    gen = torch.Generator(device=device).manual_seed(5)
+    kc = torch.randn((wb.n_pool_blocks, 16, 4, 128), generator=gen, device=device).to(torch.bfloat16)
+    vc = torch.randn(kc.shape, generator=gen, device=device).to(torch.bfloat16)
+    q = torch.randn((wb.batch, 28, 128), generator=gen, device=device).to(torch.bfloat16)
+    bt = torch.from_numpy(wb.padded_tables()).to(device)
+    sl = torch.from_numpy(wb.seq_lens.astype(np.int32)).to(device)
+    ml = int(wb.seq_lens.max())
+    plan = A.DecodePlan(bt, sl, ml, g.n_kv_heads)
+    got = A.paged_decode_attention(q, kc, vc, bt, sl, 1 / math.sqrt(128), ml, plan=plan)
+    ref = A.paged_decode_attention(q, kc, vc, bt, sl, 1 / math.sqrt(128), ml)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
+def test_plan_misuse_is_rejected(device):
+    lens = [40, 7]
+    _, _, _, _, _, q, kc, vc, bt, sl = _device_case(device, lens, 8, 2, 64, "bf16", 3)
+    plan = A.DecodePlan(bt, sl, 40, 2)
+    with pytest.raises(ValueError):  # another max_seq_len
+        A.paged_decode_attention(q, kc, vc, None, None, 0.125, 64, plan=plan)
+    with pytest.raises(ValueError):  # another workgroup count
+        A.paged_decode_attention(q, kc, vc, None, None, 0.125, 40, n_workgroups=3, plan=plan)
+    with pytest.raises(ValueError):  # tables the plan was not built from
+        A.paged_decode_attention(q, kc, vc, bt.clone(), sl, 0.125, 40, plan=plan)
+    big = torch.zeros((2500, 1), dtype=torch.int32, device=device)
+    with pytest.raises(A._lib.AegkvError):  # above one launch's batch
+        A.DecodePlan(big, torch.ones(2500, dtype=torch.int32, device=device), 16, 2)
