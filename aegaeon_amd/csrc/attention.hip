@@ -439,7 +439,7 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
                                              int id_first) {
   constexpr int KS = D / 32;
   constexpr int DPL = D / 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
   const int h = grp * kHeadsPerGroup + wave;
   if (h >= a.n_kv_heads) return;  // wave past the last kv head (uniform)
   const int j = lane & 15, g = lane >> 4;
@@ -503,6 +503,9 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   u32x4 qv[KS], qn[KS];
   load_q(bc, qv);
   int bn = cend < i1 ? next_seq(bc) : bc;
+  // A fresh load even when bn == bc: the compiler would otherwise copy qv,
+  // and the copy waits for every load in flight.
+  asm volatile("" : "+s"(bn));
   load_q(bn, qn);
 
   f32x4 acc[DPL];
