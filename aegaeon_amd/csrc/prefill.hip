@@ -126,7 +126,8 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
   const int kv_end = a.causal ? min(len, q0 + kPfQTile) : len;
   const int n_kt = (kv_end + kPfKTile - 1) / kPfKTile;
 
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the tile tests below branch
   const int col = lane & 31, hh = lane >> 5;
   const int qi = q0 + 32 * w + col;  // this lane's query, relative to the sequence
   const int wq0 = q0 + 32 * w;       // the wave's first query
