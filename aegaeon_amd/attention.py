@@ -243,6 +243,8 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
     tables and lengths (then ``block_tables``/``seq_lens`` may be None, or
     must be the tensors it was built from); the result is identical."""
     if plan is not None:
+        if plan.buffer.device != q.device:
+            raise ValueError(f"the plan lives on {plan.buffer.device}, the call on {q.device}")
         for given, held, name in ((block_tables, plan.block_tables, "block_tables"),
                                   (seq_lens, plan.seq_lens, "seq_lens")):
             if given is not None and given.data_ptr() != held.data_ptr():
