@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(AppendArgs a)
 // of a plain contiguous non-temporal copy on the same GPU.)
 constexpr int kGatherThreads = 256;
 constexpr int kGatherMaxBatch = 1024;  // sequences per launch (LDS scan)
-constexpr int kGatherWorkgroupsPerCu = 32;  // 4..32 measured within 3% (32 best)
+constexpr int kGatherWorkgroupsPerCu = 64;  // 8..256 measured: 64 best, 128 10% and 256 40% slower
 constexpr uint32_t kGatherPassBytes = kGatherThreads * 16 * 4;  // 16 KiB per pass
 
 struct GatherArgs {
@@ -113,7 +113,27 @@ struct GatherArgs {
   uint32_t block_size;
   int32_t batch;       // <= kGatherMaxBatch
   int32_t n_lk;        // 2 * n_layers
+  int32_t passes;      // 16 KiB passes per block tile (rows wider than 1 KiB: more than one)
 };
+
+// buffer descriptor word 3 of the gfx9 family (32-bit data format, no
+// swizzle) and the nontemporal cache policy bit of its buffer instructions
+constexpr int kRawBufferWord3 = 0x00020000;
+constexpr int kNt = 2;
+
+// a raw buffer range [p, p + bytes): loads past its end return zero and
+// stores past its end are dropped by the hardware's range check
+// range of the workgroup-uniform p and bytes; both are read from lane 0 so
+// the descriptor lives in scalar registers (a per-lane descriptor would make
+// the compiler loop over its distinct values)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_range(const uint8_t* p, uint32_t bytes) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  uint8_t* base = reinterpret_cast<uint8_t*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, __builtin_amdgcn_readfirstlane((int)bytes),
+                                           kRawBufferWord3);
+}
 
 __global__ __launch_bounds__(kGatherThreads) void gather_tokens_kernel(GatherArgs a) {
   __shared__ int32_t pre[kGatherMaxBatch + 1];  // first tile of each sequence
@@ -150,15 +170,20 @@ __global__ __launch_bounds__(kGatherThreads) void gather_tokens_kernel(GatherArg
   }
   if (t == kGatherThreads - 1) pre[B] = excl;  // total (B may equal the capacity)
   __syncthreads();
-  const int64_t T = pre[B];
+  // tiles: (layer*2+kv, block tile, pass), pass p covering bytes
+  // [16 KiB p, 16 KiB (p + 1)) of the block tile
+  const int64_t T = (int64_t)pre[B] * a.passes;
   const int64_t total = T * a.n_lk;
   int64_t g = blockIdx.x;
   if (g >= total) return;  // uniform
 
-  // tile g -> (lk, b, j): b is the last sequence whose first tile is <= r
-  auto locate = [&](int64_t gg, int& lk, int& b, int& j) {
+  // tile g -> (lk, b, j, pass): b is the last sequence whose first block
+  // tile is <= the tile's block index
+  auto locate = [&](int64_t gg, int& lk, int& b, int& j, int& ps) {
     lk = (int)(gg / T);
-    const int r = (int)(gg - (int64_t)lk * T);
+    int r = (int)(gg - (int64_t)lk * T);
+    ps = r % a.passes;
+    r /= a.passes;
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -168,62 +193,51 @@ __global__ __launch_bounds__(kGatherThreads) void gather_tokens_kernel(GatherArg
     b = lo;
     j = r - pre[lo];
   };
-  int lk, b, j;
-  locate(g, lk, b, j);
+  int lk, b, j, ps;
+  locate(g, lk, b, j, ps);
   int32_t id = a.block_tables[(int64_t)b * a.max_blocks + j];
   int64_t row0 = a.cu_seqlens[b];
   while (true) {
-    // current tile
+    // current tile: one straight pass of at most 16 KiB, so the loop body
+    // holds no inner loop and its vector-memory waits stay exact
     const int layer = lk >> 1, kv = lk & 1;
     const int64_t row = row0 + (int64_t)j * bs;
     int n_tok = min(bs, lens[b] - j * bs);
     if (row < 0 || row >= a.out_tokens || id < 0 || id >= a.n_blocks) n_tok = 0;
     else n_tok = (int)min((int64_t)n_tok, a.out_tokens - row);
-    const uint32_t bytes = (uint32_t)n_tok * a.row_bytes;
-    const u32x4* sp = reinterpret_cast<const u32x4*>(
-        (kv ? a.vc : a.kc) + layer * a.layer_b + (int64_t)max(id, 0) * a.blk_b);
-    u32x4* dp = reinterpret_cast<u32x4*>((kv ? a.out_v : a.out_k) + layer * a.out_layer_b +
-                                         max(row, (int64_t)0) * a.row_bytes);
+    const int64_t tile_bytes = (int64_t)n_tok * a.row_bytes - (int64_t)ps * kGatherPassBytes;
+    const uint32_t bytes = (uint32_t)max((int64_t)0, min(tile_bytes, (int64_t)kGatherPassBytes));
+    const uint64_t pass_off = (uint64_t)ps * kGatherPassBytes;
+    // raw buffer ranges of `bytes` bytes: the hardware's range check drops
+    // the lanes past the end, so every load and store below issues and the
+    // compiler counts them exactly (no exec branches around memory)
+    const auto src = byte_range(
+        (kv ? a.vc : a.kc) + layer * a.layer_b + (int64_t)max(id, 0) * a.blk_b + pass_off, bytes);
+    const auto dst = byte_range((kv ? a.out_v : a.out_k) + layer * a.out_layer_b +
+                                    max(row, (int64_t)0) * a.row_bytes + pass_off,
+                                bytes);
     u32x4 r[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t c = k * kGatherThreads + t;
-      if (c * 16 < bytes) r[k] = __builtin_nontemporal_load(sp + c);
-    }
-    // next tile's id and output row, in flight with the loads above
+    for (int k = 0; k < 4; ++k)
+      r[k] = __builtin_amdgcn_raw_buffer_load_b128(src, (k * kGatherThreads + t) * 16, 0, kNt);
+    // next tile's id and output row, in flight with the loads above; issued
+    // unconditionally (the last tile locates itself again), since a load
+    // under a branch would make the stores below wait for it
     const int64_t gn = g + gridDim.x;
     const bool more = gn < total;
-    int nlk = lk, nb = b, nj = j;
-    int32_t nid = id;
-    int64_t nrow0 = row0;
-    if (more) {
-      locate(gn, nlk, nb, nj);
-      nid = a.block_tables[(int64_t)nb * a.max_blocks + nj];
-      nrow0 = a.cu_seqlens[nb];
-    }
+    int nlk, nb, nj, nps;
+    locate(more ? gn : g, nlk, nb, nj, nps);
+    const int32_t nid = a.block_tables[(int64_t)nb * a.max_blocks + nj];
+    const int64_t nrow0 = a.cu_seqlens[nb];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t c = k * kGatherThreads + t;
-      if (c * 16 < bytes) __builtin_nontemporal_store(r[k], dp + c);
-    }
-    // rows wider than 1 KiB: the rest of the tile, 16 KiB per pass
-    for (uint32_t base = kGatherPassBytes / 16; base * 16 < bytes; base += kGatherPassBytes / 16) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t c = base + k * kGatherThreads + t;
-        if (c * 16 < bytes) r[k] = __builtin_nontemporal_load(sp + c);
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t c = base + k * kGatherThreads + t;
-        if (c * 16 < bytes) __builtin_nontemporal_store(r[k], dp + c);
-      }
-    }
+    for (int k = 0; k < 4; ++k)
+      __builtin_amdgcn_raw_buffer_store_b128(r[k], dst, (k * kGatherThreads + t) * 16, 0, kNt);
     if (!more) break;
     g = gn;
     lk = nlk;
     b = nb;
     j = nj;
+    ps = nps;
     id = nid;
     row0 = nrow0;
   }
@@ -310,7 +324,8 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
     return AEGKV_ERR_MISALIGNED;
   const int64_t blocks_needed = ((int64_t)max_seq_len + block_size - 1) / block_size;
   if (blocks_needed > max_blocks) return AEGKV_ERR_INVALID_ARG;
-  if (blocks_needed * kGatherMaxBatch > INT32_MAX || (int64_t)n_layers * 2 > 65535)
+  const int64_t passes = ((int64_t)block_size * row_bytes + kGatherPassBytes - 1) / kGatherPassBytes;
+  if (blocks_needed * kGatherMaxBatch * passes > INT32_MAX || (int64_t)n_layers * 2 > 65535)
     return AEGKV_ERR_UNSUPPORTED;
   DeviceState* ds = nullptr;
   int rc = current_device_state(&ds);
@@ -330,6 +345,7 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
   a.row_bytes = (uint32_t)row_bytes;
   a.block_size = (uint32_t)block_size;
   a.n_lk = 2 * n_layers;
+  a.passes = (int32_t)passes;
   const int64_t max_grid = (int64_t)std::max(ds->num_cu, 1) * kGatherWorkgroupsPerCu;
   for (int32_t b0 = 0; b0 < batch; b0 += kGatherMaxBatch) {
     const int32_t nb = std::min(kGatherMaxBatch, batch - b0);
@@ -337,7 +353,7 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
     a.block_tables = block_tables + (int64_t)b0 * max_blocks;
     a.seq_lens = seq_lens + b0;
     a.cu_seqlens = cu_seqlens + b0;
-    const int64_t tiles_max = blocks_needed * nb * a.n_lk;  // upper bound of the tiles
+    const int64_t tiles_max = blocks_needed * nb * a.n_lk * a.passes;  // bound of the tiles
     const uint32_t grid = (uint32_t)std::max<int64_t>(1, std::min(tiles_max, max_grid));
     hipLaunchKernelGGL(gather_tokens_kernel, dim3(grid), dim3(kGatherThreads), 0,
                        (hipStream_t)stream, a);
