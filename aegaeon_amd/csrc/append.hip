@@ -79,17 +79,15 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(AppendArgs a)
   }
 }
 
-// One workgroup per (logical block, sequence, layer*2+kv): the tokens of a
-// block are contiguous rows in both the cache and the output, so the work is a
-// straight copy of n_tok * row bytes.
-// gather_tokens: a tile is one logical block (<= block_size tokens) of one
+// gather_tokens: the tokens of a logical block (<= block_size tokens) are
+// contiguous rows in both the cache and the output, so a block is a straight
+// copy of n_tok * row bytes.  A tile is one 16 KiB pass of one block of one
 // sequence for one (layer, K/V).  Each workgroup scans the batch's tile counts
 // into LDS, then a persistent grid walks the flattened (layer, K/V, sequence,
-// block) tiles round-robin; the block id and output row of a workgroup's next
-// tile are fetched while the current tile's non-temporal loads are in flight.
-// (One workgroup per tile spent a dependent id load per 16 KiB and ran at
-// 4.9 TB/s on the Qwen2.5-7B batch; this walk reaches 5.3-5.4 TB/s, about 86%
-// of a plain contiguous non-temporal copy on the same GPU.)
+// block, pass) tiles round-robin; the block id and output row of a workgroup's
+// next tile are fetched while the current tile's non-temporal loads are in
+// flight.  (One workgroup per block spent a dependent id load per 16 KiB and
+// ran at 4.9 TB/s on the Qwen2.5-7B batch; this walk reaches 5.6 TB/s.)
 constexpr int kGatherThreads = 256;
 constexpr int kGatherMaxBatch = 1024;  // sequences per launch (LDS scan)
 constexpr int kGatherWorkgroupsPerCu = 64;  // 8..256 measured: 64 best, 128 10% and 256 40% slower
