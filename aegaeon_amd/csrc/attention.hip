@@ -876,13 +876,17 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
 // The kv head's G query heads x D/4 float4 columns are "items", spread densely
 // over the 64 lanes of a wave (KI = ceil(G * D/4 / 64) per lane, a template
 // parameter so that registers follow the group size); wave w merges pieces
-// w, w + 4, ... online (two loaded at a time, so four waves cover eight pieces
-// per memory round trip), and the four waves' states merge in LDS.
+// w, w + 4, ... online, one at a time, and the four waves' states merge in LDS.
+// Most of the grid's workgroups hold no task and exit after the descriptor
+// load, so what bounds the kernel is how many of them a CU holds at once: one
+// piece per load round keeps the kernel at 91 VGPRs and every workgroup
+// resident (Qwen2.5-7B batch: two pieces per round, 156 VGPRs, measured
+// 0.5 us per layer slower; four, 268 VGPRs, 8 us slower).
 template <int DT, int D, int KI>
 __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(AttnArgs a) {
   using E = Elem<DT>;
   constexpr int D4 = D / 4;                // float4 per query head
-  constexpr int U = KI >= 8 ? 1 : 2;       // pieces loaded together per wave
+  constexpr int U = 1;                     // pieces loaded together per wave
   __shared__ float s_m[kHeadsPerGroup - 1][KI][64];
   __shared__ float s_l[kHeadsPerGroup - 1][KI][64];
   __shared__ f32x4 s_o[kHeadsPerGroup - 1][KI][64];
