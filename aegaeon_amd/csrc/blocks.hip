@@ -10,7 +10,11 @@
 // dwordx4 loads before the four stores (4 KiB in flight per wave, every
 // access a fully coalesced 1 KiB wave row).  The block ids of a workgroup's
 // next tile are loaded together with the current tile's data, so no tile waits
-// on an id load in front of its own loads.
+// on an id load in front of its own loads.  Loads and stores are raw buffer
+// instructions bounded to the tile's valid bytes (no exec branches around
+// memory), which keeps the compiler's wait counts exact: a store waits for its
+// own load only (measured 4% faster on a contiguous 256 MiB copy than the
+// same loop with masked global loads and stores).
 #include <algorithm>
 #include <numeric>
 
@@ -27,6 +31,29 @@ constexpr uint64_t kTileBytes = (uint64_t)kCopyThreads * 16 * kCopyUnroll;  // 1
 constexpr int kCopyWorkgroupsPerCu = 32;  // measured best of 2..32 with chunks 1..64 tiles
 constexpr int kCopyChunkTiles = 1;  // 0 = one contiguous range per workgroup
 
+// buffer descriptor word 3 of the gfx9 family (32-bit data format, no
+// swizzle) and the nontemporal cache policy bit of its buffer instructions
+constexpr int kRawBufferWord3 = 0x00020000;
+constexpr int kNt = 2;
+
+// A raw buffer range [p, p + bytes) of the workgroup-uniform p and bytes (read
+// from lane 0, so the descriptor lives in scalar registers): loads past its
+// end return zero and stores past its end are dropped by the hardware's range
+// check, so a partial tile needs no exec branch around its memory accesses.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_range(const uint8_t* p, uint32_t bytes) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  uint8_t* base = reinterpret_cast<uint8_t*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, __builtin_amdgcn_readfirstlane((int)bytes),
+                                           kRawBufferWord3);
+}
+
+// SRC_IDS / DST_IDS: whether the side is addressed through an id list (else
+// block i of the side is slot i).  Every memory access of the loop is issued
+// unconditionally, so the compiler's wait counts are exact: the stores wait
+// only for their own tile's loads and the loop head only for the next ids.
+template <bool SRC_IDS, bool DST_IDS>
 __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
     const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
     const int64_t* __restrict__ src_ids, const int64_t* __restrict__ dst_ids,
@@ -37,8 +64,8 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
   if (tile >= n_tiles) return;
   uint64_t chunk_end = min(tile + chunk_tiles, n_tiles);
   uint64_t i = tile / tiles_per_block;  // block index of the current tile
-  int64_t s = src_ids ? src_ids[i] : (int64_t)i;
-  int64_t d = dst_ids ? dst_ids[i] : (int64_t)i;
+  int64_t s = SRC_IDS ? src_ids[i] : (int64_t)i;
+  int64_t d = DST_IDS ? dst_ids[i] : (int64_t)i;
   while (true) {
     uint64_t next = tile + 1, next_end = chunk_end;
     if (next >= chunk_end) {  // first tile of this workgroup's next chunk
@@ -47,26 +74,23 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
     }
     const bool more = next < n_tiles;
     const uint64_t ni = more ? next / tiles_per_block : i;
-    int64_t ns = s, nd = d;
-    if (ni != i) {
-      ns = src_ids ? src_ids[ni] : (int64_t)ni;
-      nd = dst_ids ? dst_ids[ni] : (int64_t)ni;
-    }
     const uint64_t base = (tile - i * tiles_per_block) * kTileBytes;
-    const uint64_t rem = block_bytes - base;  // bytes of this block from the tile start
-    const u32x4* sp = reinterpret_cast<const u32x4*>(src + (uint64_t)s * block_bytes + base);
-    u32x4* dp = reinterpret_cast<u32x4*>(dst + (uint64_t)d * block_bytes + base);
+    const uint32_t bytes = (uint32_t)min(block_bytes - base, kTileBytes);
+    const auto sr = byte_range(src + (uint64_t)s * block_bytes + base, bytes);
+    const auto dr = byte_range(dst + (uint64_t)d * block_bytes + base, bytes);
     u32x4 r[kCopyUnroll];
 #pragma unroll
-    for (int k = 0; k < kCopyUnroll; ++k) {
-      const uint32_t c = k * kCopyThreads + threadIdx.x;
-      if ((uint64_t)c * 16 < rem) r[k] = __builtin_nontemporal_load(sp + c);
-    }
+    for (int k = 0; k < kCopyUnroll; ++k)
+      r[k] = __builtin_amdgcn_raw_buffer_load_b128(sr, (k * kCopyThreads + threadIdx.x) * 16, 0,
+                                                   kNt);
+    // the next tile's ids (the same block's again, mostly: an L2 hit), in
+    // flight with the loads above
+    const int64_t ns = SRC_IDS ? src_ids[ni] : (int64_t)ni;
+    const int64_t nd = DST_IDS ? dst_ids[ni] : (int64_t)ni;
 #pragma unroll
-    for (int k = 0; k < kCopyUnroll; ++k) {
-      const uint32_t c = k * kCopyThreads + threadIdx.x;
-      if ((uint64_t)c * 16 < rem) __builtin_nontemporal_store(r[k], dp + c);
-    }
+    for (int k = 0; k < kCopyUnroll; ++k)
+      __builtin_amdgcn_raw_buffer_store_b128(r[k], dr, (k * kCopyThreads + threadIdx.x) * 16, 0,
+                                             kNt);
     if (!more) break;
     tile = next;
     chunk_end = next_end;
@@ -89,7 +113,11 @@ int launch_copy_blocks(const DeviceState* ds, const void* src, void* dst,
                                              : (n_tiles + max_grid - 1) / max_grid;
   const uint64_t n_chunks = (n_tiles + chunk - 1) / chunk;
   const uint32_t grid = (uint32_t)std::min<uint64_t>(n_chunks, max_grid);
-  hipLaunchKernelGGL(copy_blocks_kernel, dim3(grid), dim3(kCopyThreads), 0, stream,
+  auto kernel = src_ids_dev ? (dst_ids_dev ? copy_blocks_kernel<true, true>
+                                            : copy_blocks_kernel<true, false>)
+                            : (dst_ids_dev ? copy_blocks_kernel<false, true>
+                                           : copy_blocks_kernel<false, false>);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kCopyThreads), 0, stream,
                      static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst),
                      src_ids_dev, dst_ids_dev, block_bytes, (uint32_t)tiles_per_block,
                      n_tiles, chunk);
