@@ -500,13 +500,8 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
     return b;
   };
 
-  u32x4 qv[KS], qn[KS];
+  u32x4 qv[KS];
   load_q(bc, qv);
-  int bn = cend < i1 ? next_seq(bc) : bc;
-  // A fresh load even when bn == bc: the compiler would otherwise copy qv,
-  // and the copy waits for every load in flight.
-  asm volatile("" : "+s"(bn));
-  load_q(bn, qn);
 
   f32x4 acc[DPL];
 #pragma unroll
@@ -549,15 +544,12 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
         store_piece<DT, D>(a, acc, m, lt, bc, hq, complete, pslot, hl0);
       }
       if (ic < i1) {
-        bc = bn;
+        bc = next_seq(bc);
         first = uni(s_bcum[bc]);
         cend = min(uni(s_bcum[bc + 1]), i1);
         len = uni(s_len[bc]);
         complete = cend == uni(s_bcum[bc + 1]);  // it starts in range
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qv[ks] = qn[ks];
-        bn = cend < i1 ? next_seq(bc) : bc;
-        load_q(bn, qn);
+        load_q(bc, qv);
 #pragma unroll
         for (int t = 0; t < DPL; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         m = -INFINITY;
