@@ -96,6 +96,27 @@ int with_uploaded_ids(DeviceState* ds, hipStream_t stream, const IdPart* parts,
   return rc;
 }
 
+// Raw buffer ranges for the byte-moving kernels.  kRawBufferWord3 is word 3
+// of a gfx9-family buffer descriptor (32-bit data format, no swizzle); kNt is
+// the nontemporal cache-policy bit of its buffer instructions.
+constexpr int kRawBufferWord3 = 0x00020000;
+constexpr int kNt = 2;
+
+// A raw buffer range [p, p + bytes) of the workgroup-uniform p and bytes, both
+// read from lane 0 so the descriptor lives in scalar registers (a per-lane
+// descriptor would make the compiler loop over its distinct values).  Loads
+// past its end return zero and stores past its end are dropped by the
+// hardware's range check, so a partial tile needs no exec branch around its
+// memory accesses and the compiler's vector-memory wait counts stay exact.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_range(const uint8_t* p, uint32_t bytes) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  uint8_t* base = reinterpret_cast<uint8_t*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, __builtin_amdgcn_readfirstlane((int)bytes),
+                                           kRawBufferWord3);
+}
+
 // Block-copy launcher shared by pack/scatter/copy/defrag/swap:
 // dst[dst_ids ? dst_ids[i] : dst_base_index + i] <- src[src_ids ? src_ids[i] : src_base_index + i]
 // for i in [0, n); the id arrays are DEVICE pointers (or null).

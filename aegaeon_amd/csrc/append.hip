@@ -114,25 +114,6 @@ struct GatherArgs {
   int32_t passes;      // 16 KiB passes per block tile (rows wider than 1 KiB: more than one)
 };
 
-// buffer descriptor word 3 of the gfx9 family (32-bit data format, no
-// swizzle) and the nontemporal cache policy bit of its buffer instructions
-constexpr int kRawBufferWord3 = 0x00020000;
-constexpr int kNt = 2;
-
-// a raw buffer range [p, p + bytes): loads past its end return zero and
-// stores past its end are dropped by the hardware's range check
-// range of the workgroup-uniform p and bytes; both are read from lane 0 so
-// the descriptor lives in scalar registers (a per-lane descriptor would make
-// the compiler loop over its distinct values)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_range(const uint8_t* p, uint32_t bytes) {
-  const uint64_t u = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-  uint8_t* base = reinterpret_cast<uint8_t*>(((uint64_t)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(base, 0, __builtin_amdgcn_readfirstlane((int)bytes),
-                                           kRawBufferWord3);
-}
-
 __global__ __launch_bounds__(kGatherThreads) void gather_tokens_kernel(GatherArgs a) {
   __shared__ int32_t pre[kGatherMaxBatch + 1];  // first tile of each sequence
   __shared__ int32_t lens[kGatherMaxBatch];

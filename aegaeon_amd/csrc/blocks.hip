@@ -31,24 +31,6 @@ constexpr uint64_t kTileBytes = (uint64_t)kCopyThreads * 16 * kCopyUnroll;  // 1
 constexpr int kCopyWorkgroupsPerCu = 32;  // measured best of 2..32 with chunks 1..64 tiles
 constexpr int kCopyChunkTiles = 1;  // 0 = one contiguous range per workgroup
 
-// buffer descriptor word 3 of the gfx9 family (32-bit data format, no
-// swizzle) and the nontemporal cache policy bit of its buffer instructions
-constexpr int kRawBufferWord3 = 0x00020000;
-constexpr int kNt = 2;
-
-// A raw buffer range [p, p + bytes) of the workgroup-uniform p and bytes (read
-// from lane 0, so the descriptor lives in scalar registers): loads past its
-// end return zero and stores past its end are dropped by the hardware's range
-// check, so a partial tile needs no exec branch around its memory accesses.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_range(const uint8_t* p, uint32_t bytes) {
-  const uint64_t u = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-  uint8_t* base = reinterpret_cast<uint8_t*>(((uint64_t)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(base, 0, __builtin_amdgcn_readfirstlane((int)bytes),
-                                           kRawBufferWord3);
-}
-
 // SRC_IDS / DST_IDS: whether the side is addressed through an id list (else
 // block i of the side is slot i).  Every memory access of the loop is issued
 // unconditionally, so the compiler's wait counts are exact: the stores wait
