@@ -734,8 +734,9 @@ def main(argv=None):
                         "prepare,bm,calib or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the KV data path is per-GPU and "
-                                   "runs no collectives, so --gpus must be 1"}), flush=True)
+        print(json.dumps({"error": "aegaeon_amd's KV data path is per-GPU and runs no "
+                                   "collectives: the benchmark measures one GPU, so --gpus must "
+                                   "be 1"}), flush=True)
         return 2
     import torch
     if not torch.cuda.is_available():
