@@ -3,8 +3,9 @@
 A numpy restatement of the reference's semantics for every op of the path
 (swap, slot mapping, append, gather, pack/scatter, defrag, paged decode
 attention).  Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-``cpu_baseline`` leg may import it, and only as the checker or the timed CPU
-baseline; the product package (``aegaeon_amd``) never imports it.
+``cpu_baseline`` leg may import it, and only as the reference that results are
+compared with or as the timed CPU baseline; the product package
+(``aegaeon_amd``) never imports it.
 
 Pinning (what fixes each function independently of this file's formulas):
   swap_blocks, copy_blocks, pack/scatter  - brute-force per-byte loops in

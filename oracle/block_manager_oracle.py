@@ -1,6 +1,6 @@
 """Pure-Python restatement of the reference's block-manager bookkeeping
-(aegaeon/aegaeon/block_manager.py) — test infrastructure, the checker of the
-native block manager, never on the product path.
+(aegaeon/aegaeon/block_manager.py) — test infrastructure that the native
+block manager's results are compared with, never on the product path.
 
 Restated synchronously: where the reference awaits the completion of pending
 moves (_reclaim_blocks, block_manager.py:360-408), this class calls
