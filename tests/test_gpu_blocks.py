@@ -86,6 +86,25 @@ def test_pack_scatter_copy(device, block_bytes):
     assert np.array_equal(third.cpu().numpy(), ref3)
 
 
+@pytest.mark.parametrize("block_bytes", [16400, 917504])
+def test_copy_without_id_lists(device, block_bytes):
+    """aegkv_copy_blocks with both id lists null copies blocks 0..n-1 of one pool
+    into another (the C ABI's identity form; partial last tile at 16400 bytes),
+    leaving the blocks past n untouched."""
+    from aegaeon_amd import _lib
+    rng = np.random.default_rng(block_bytes + 1)
+    N, n = 12, 7
+    src_np = rng.integers(0, 256, size=(N, block_bytes), dtype=np.uint8)
+    src = torch.from_numpy(src_np).to(device)
+    dst = torch.full_like(src, 0xA5)
+    rc = _lib.load().aegkv_copy_blocks(src.data_ptr(), N, dst.data_ptr(), N, None, None, n,
+                                       block_bytes, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    ref = np.full_like(src_np, 0xA5)
+    ref[:n] = src_np[:n]
+    assert np.array_equal(dst.cpu().numpy(), ref)
+
+
 def test_defrag_in_place(device):
     rng = np.random.default_rng(3)
     N, bb = 200, 4096
