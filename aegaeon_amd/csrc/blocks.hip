@@ -90,7 +90,14 @@ int launch_copy_blocks(const DeviceState* ds, const void* src, void* dst,
   if (n <= 0) return AEGKV_OK;
   const uint64_t tiles_per_block = (block_bytes + kTileBytes - 1) / kTileBytes;
   const uint64_t n_tiles = tiles_per_block * (uint64_t)n;
-  const uint64_t max_grid = (uint64_t)std::max(ds->num_cu, 1) * kCopyWorkgroupsPerCu;
+  // A contiguous source scattered by destination ids (scatter, swap-in) runs
+  // one short-lived workgroup per tile: Llama-2-13B 4096 x 12.5 MiB blocks,
+  // 6.52 TB/s against 6.19 TB/s with the persistent grid.  Pack, copy and defrag
+  // keep the persistent grid (pack measured 5% slower with a tile per
+  // workgroup).
+  const bool per_tile = !src_ids_dev && dst_ids_dev;
+  const uint64_t max_grid =
+      per_tile ? (1ull << 30) : (uint64_t)std::max(ds->num_cu, 1) * kCopyWorkgroupsPerCu;
   const uint64_t chunk = kCopyChunkTiles > 0 ? (uint64_t)kCopyChunkTiles
                                              : (n_tiles + max_grid - 1) / max_grid;
   const uint64_t n_chunks = (n_tiles + chunk - 1) / chunk;
