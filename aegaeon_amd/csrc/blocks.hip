@@ -4,9 +4,10 @@
 //
 // One kernel serves every device-side move.  A block of block_bytes is cut into
 // 16 KiB tiles and the tiles of all blocks are laid end to end, then grouped
-// into chunks of chunk_tiles consecutive tiles; a persistent grid of G
-// workgroups deals the chunks round-robin (workgroup w copies chunks w, w + G,
-// ...), one tile per iteration.  Per tile, each lane issues four non-temporal
+// into chunks of chunk_tiles consecutive tiles; a grid of G workgroups deals
+// the chunks round-robin (workgroup w copies chunks w, w + G, ...), one tile
+// per iteration.  G is 32 per CU (persistent), or one per tile when the
+// source is contiguous and only the destination goes through ids (scatter).  Per tile, each lane issues four non-temporal
 // dwordx4 loads before the four stores (4 KiB in flight per wave, every
 // access a fully coalesced 1 KiB wave row).  The block ids of a workgroup's
 // next tile are loaded together with the current tile's data, so no tile waits
