@@ -121,6 +121,51 @@ def test_defrag_in_place(device):
         assert np.array_equal(got[new], pool_np[old])
 
 
+def test_llama_full_size_swap_round_trip(device):
+    """Llama-2-13B at full size (40 layers, 40 kv heads, D 128, fp16, 32
+    sequences of 2048 tokens = 4096 blocks of 12.5 MiB in a pool of 8192):
+    pack the scattered blocks, scatter them into a disjoint seeded free set,
+    and check bit-exactness block by block on both sides; then a sampled host
+    leg (64 blocks) through ops.swap out to pinned memory and back in.  The
+    property (a move reproduces its bytes and touches nothing else) holds
+    at any size; this runs it at the workload's."""
+    from aegaeon_amd.workloads import llama_swap_workload
+    wl = llama_swap_workload(0)
+    bb = wl.geometry.block_bytes
+    need = (wl.n_pool_blocks + wl.n_blocks) * bb
+    torch.cuda.empty_cache()
+    if torch.cuda.get_device_properties(device).total_memory < need + (16 << 30):
+        pytest.skip("needs %d GiB of device memory" % ((need >> 30) + 16))
+    pool = torch.empty((wl.n_pool_blocks, bb), dtype=torch.uint8, device=device)
+    pool.view(torch.int32).random_(generator=torch.Generator(device=device).manual_seed(5))
+    src = np.asarray(wl.gpu_ids, dtype=np.int64)
+    dst = np.asarray(wl.swap_in_ids, dtype=np.int64)
+    assert not set(src.tolist()) & set(dst.tolist())
+    untouched = np.setdiff1d(np.arange(wl.n_pool_blocks), np.concatenate([src, dst]))
+    keep = torch.from_numpy(untouched[:64]).to(device)
+    before = pool[keep].clone()
+    staging = ops.pack_blocks(pool, src)
+    ops.scatter_blocks(staging, dst, pool)
+    torch.cuda.synchronize()
+    for c in range(0, wl.n_blocks, 256):
+        i = torch.arange(c, min(c + 256, wl.n_blocks), device=device)
+        assert torch.equal(pool[torch.from_numpy(dst[c:c + 256]).to(device)], staging[i])
+        assert torch.equal(pool[torch.from_numpy(src[c:c + 256]).to(device)], staging[i])
+    assert torch.equal(pool[keep], before)
+    del staging
+    # host leg on a sample: out to pinned memory, back in to other free ids
+    n_s = 64
+    host = torch.zeros((n_s, bb), dtype=torch.uint8, pin_memory=True)
+    ops.swap(src[:n_s], np.arange(n_s), False, pool, host)
+    ops.swap(np.arange(n_s), dst[n_s:2 * n_s], True, pool, host)
+    torch.cuda.synchronize()
+    assert torch.equal(host.to(device), pool[torch.from_numpy(src[:n_s]).to(device)])
+    assert torch.equal(pool[torch.from_numpy(dst[n_s:2 * n_s]).to(device)],
+                       pool[torch.from_numpy(src[:n_s]).to(device)])
+    del pool, host, before
+    torch.cuda.empty_cache()
+
+
 def test_empty_lists_are_noops(device):
     cache = torch.zeros((4, 2, 16, 1, 64), dtype=torch.float16, device=device)
     host = torch.zeros((4, 2, 16, 1, 64), dtype=torch.float16, pin_memory=True)
