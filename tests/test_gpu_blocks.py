@@ -166,6 +166,55 @@ def test_llama_full_size_swap_round_trip(device):
     torch.cuda.empty_cache()
 
 
+def test_unified_pool_full_size_defrag(device):
+    """The unified pool at full size (44 GiB: Yi-1.5-9B, Qwen2.5-7B and
+    Llama-2-13B blocks in 1 GiB slabs, 50% live): each model's live blocks are
+    compacted into the dense prefix of its id space.  Every live block's bytes
+    reappear, bit-exact, at its remapped id, the new ids form the prefix, and
+    the free blocks that received nothing keep their bytes."""
+    from aegaeon_amd.pool import plan_compaction, remap_tables
+    from aegaeon_amd.workloads import unified_pool_workload
+    wl = unified_pool_workload(0)
+    torch.cuda.empty_cache()
+    if torch.cuda.get_device_properties(device).total_memory < 2 * wl.pool_bytes + (16 << 30):
+        pytest.skip("needs %d GiB of device memory" % ((2 * wl.pool_bytes >> 30) + 16))
+    pool = torch.empty(wl.pool_bytes, dtype=torch.uint8, device=device)
+    pool.view(torch.int32).random_(generator=torch.Generator(device=device).manual_seed(6))
+    before = pool.clone()
+
+    def blocks(t, bb):
+        nb = wl.pool_bytes // bb
+        return t[:nb * bb].view(nb, bb)
+
+    def same(a_ids, b_ids, bb):
+        a_ids, b_ids = np.asarray(a_ids, dtype=np.int64), np.asarray(b_ids, dtype=np.int64)
+        for c in range(0, len(a_ids), 128):
+            ia = torch.from_numpy(a_ids[c:c + 128]).to(device)
+            ib = torch.from_numpy(b_ids[c:c + 128]).to(device)
+            if not torch.equal(blocks(pool, bb)[ia], blocks(before, bb)[ib]):
+                return False
+        return True
+
+    moved = 0
+    for name, g in wl.geometries.items():
+        bb = g.block_bytes
+        valid = list(wl.valid_ids(name))
+        src, dst = plan_compaction([b for t in wl.tables[name] for b in t], valid)
+        ops.defrag_blocks(pool, src, dst, block_bytes=bb)
+        torch.cuda.synchronize()
+        moved += len(src)
+        tables = remap_tables(wl.tables[name], src, dst)
+        old_ids = [b for t in wl.tables[name] for b in t]
+        new_ids = [b for t in tables for b in t]
+        assert sorted(new_ids) == valid[:len(new_ids)], name
+        assert same(new_ids, old_ids, bb), name
+        free = sorted(set(valid) - set(old_ids) - set(int(x) for x in dst))
+        assert same(free, free, bb), name
+    assert moved == 2047 + 2332 + 499
+    del pool, before
+    torch.cuda.empty_cache()
+
+
 def test_empty_lists_are_noops(device):
     cache = torch.zeros((4, 2, 16, 1, 64), dtype=torch.float16, device=device)
     host = torch.zeros((4, 2, 16, 1, 64), dtype=torch.float16, pin_memory=True)
