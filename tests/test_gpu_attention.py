@@ -322,3 +322,55 @@ def test_plan_misuse_is_rejected(device):
     big = torch.zeros((2500, 1), dtype=torch.int32, device=device)
     with pytest.raises(A._lib.AegkvError):  # above one launch's batch
         A.DecodePlan(big, torch.ones(2500, dtype=torch.int32, device=device), 16, 2)
+
+
+def test_yi_decode_after_unified_pool_defrag(device):
+    """The unified-pool decode step at full size: a 44 GiB byte pool of bf16
+    values co-hosting three models, the Yi-1.5-9B blocks compacted into their
+    dense prefix, then layer 0's decode attention for the 64 Yi sequences
+    (GQA 32/4, lognormal mean 1000) through a plan over the rewritten tables,
+    read from the reference's [N, L, 2, 16, Hkv, D] storage as a strided view.
+    Checked against the float64 oracle on the K/V taken before the moves,
+    through the original tables."""
+    from aegaeon_amd import ops
+    from aegaeon_amd.pool import plan_compaction, remap_tables
+    from aegaeon_amd.workloads import unified_pool_workload
+    wl = unified_pool_workload(0)
+    g = wl.geometries[wl.decode_model]
+    bb = g.block_bytes
+    torch.cuda.empty_cache()
+    if torch.cuda.get_device_properties(device).total_memory < wl.pool_bytes + (16 << 30):
+        pytest.skip("needs %d GiB of device memory" % ((wl.pool_bytes >> 30) + 16))
+    gen = torch.Generator(device=device).manual_seed(7)
+    pool = torch.empty(wl.pool_bytes, dtype=torch.uint8, device=device)
+    pool.view(torch.bfloat16).normal_(generator=gen)
+    nb = wl.pool_bytes // bb
+    typed = pool[:nb * bb].view(torch.bfloat16).view(nb, *g.block_shape)
+    old_tables = wl.tables[wl.decode_model]
+    used = sorted({b for t in old_tables for b in t})
+    idx = torch.tensor(used, device=device)
+    k_used = to_bits(typed[idx, 0, 0])                  # layer 0, K: [n, 16, Hkv, D]
+    v_used = to_bits(typed[idx, 0, 1])
+    src, dst = plan_compaction([b for t in old_tables for b in t],
+                               wl.valid_ids(wl.decode_model))
+    ops.defrag_blocks(pool, src, dst, block_bytes=bb)
+    tables = remap_tables(old_tables, src, dst)
+    lens = np.asarray(wl.yi_context_lens, dtype=np.int64)
+    q = torch.randn((len(lens), g.n_q_heads, g.head_dim), generator=gen,
+                    device=device).to(torch.bfloat16)
+    view = typed.permute(1, 2, 0, 3, 4, 5)
+    bt = torch.from_numpy(ko.pad_block_tables(tables)).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    ml = int(lens.max())
+    scale = 1 / math.sqrt(g.head_dim)
+    plan = A.DecodePlan(bt, sl, ml, g.n_kv_heads)
+    out = A.paged_decode_attention(q, view[0, 0], view[0, 1], None, None, scale, ml, plan=plan)
+    torch.cuda.synchronize()
+    pos = {b: i for i, b in enumerate(used)}
+    compact = ko.pad_block_tables([[pos[b] for b in t] for t in old_tables])
+    ref = ko.paged_decode_attention(ko.bits_to_float(to_bits(q), "bf16"),
+                                    ko.bits_to_float(k_used, "bf16"),
+                                    ko.bits_to_float(v_used, "bf16"), compact, lens, scale)
+    _check(to_bits(out), ref, "bf16")
+    del pool, typed, view
+    torch.cuda.empty_cache()
