@@ -39,6 +39,12 @@ def _check_cache_view(c: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name}: each block must hold dense [block_size, Hkv, D] rows")
 
 
+def _check_on(t: torch.Tensor, name: str, device: torch.device) -> None:
+    """A metadata tensor the kernel reads must live on the kernel's GPU."""
+    if not t.is_cuda or t.device != device:
+        raise ValueError(f"{name} must be a GPU tensor on {device} (got {t.device})")
+
+
 def _check_rows(x: torch.Tensor, name: str) -> None:
     if not x.is_cuda or x.stride(-1) != 1 or x.stride(-2) != x.size(-1):
         raise ValueError(f"{name}: rows [Hkv, D] must be dense on the GPU")
@@ -65,6 +71,14 @@ def reshape_and_cache_flash(key: torch.Tensor, value: torch.Tensor, key_cache: t
         raise ValueError("key_cache and value_cache must share the block stride")
     if slot_mapping.dtype != torch.int64 or not slot_mapping.is_cuda:
         raise ValueError("slot_mapping must be an int64 GPU tensor")
+    for t, n in ((key, "key"), (value, "value"), (value_cache, "value_cache"),
+                 (slot_mapping, "slot_mapping")):
+        _check_on(t, n, key_cache.device)
+    if key.dtype != key_cache.dtype or value.dtype != key_cache.dtype \
+            or value_cache.dtype != key_cache.dtype or key.element_size() != 2:
+        raise ValueError("key, value and the caches must share one 16-bit dtype")
+    if key.dim() != 3 or value.shape != key.shape or key.shape[1:] != key_cache.shape[2:]:
+        raise ValueError("key/value must be [T, Hkv, D] matching the cache view")
     T = key.size(0)
     N, bs, H, D = key_cache.shape
     slot_mapping = slot_mapping.contiguous()
@@ -92,6 +106,10 @@ def append_kv(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     _check_rows(value, "value")
     if slot_mapping.dtype != torch.int64 or not slot_mapping.is_cuda:
         raise ValueError("slot_mapping must be an int64 GPU tensor")
+    for t, n in ((key, "key"), (value, "value"), (slot_mapping, "slot_mapping")):
+        _check_on(t, n, kv_cache.device)
+    if key.dtype != kv_cache.dtype or value.dtype != kv_cache.dtype or key.element_size() != 2:
+        raise ValueError("key, value and kv_cache must share one 16-bit dtype")
     slot_mapping = slot_mapping.contiguous()
     T = key.size(1)
     kv_stride = bs * H * D
@@ -123,11 +141,21 @@ def gather_tokens(kv_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: 
     first, count = layers if layers is not None else (0, L)
     if not (0 <= first and first + count <= L and count > 0):
         raise ValueError("layer range out of bounds")
-    bt = block_tables.to(torch.int32).contiguous()
-    sl = seq_lens.to(torch.int32).contiguous()
+    dev = kv_cache.device
+    _check_on(block_tables, "block_tables", dev)
+    _check_on(seq_lens, "seq_lens", dev)
+    if block_tables.dim() != 2 or seq_lens.dim() != 1 or block_tables.size(0) != seq_lens.numel():
+        raise ValueError("block_tables must be [B, max_blocks] and seq_lens [B]")
+    bt = _int32_dense(block_tables)
+    sl = _int32_dense(seq_lens)
     if cu_seqlens is None:
-        cu_seqlens = torch.zeros(sl.numel() + 1, dtype=torch.int32, device=sl.device)
+        cu_seqlens = torch.zeros(sl.numel() + 1, dtype=torch.int32, device=dev)
         torch.cumsum(sl, 0, dtype=torch.int32, out=cu_seqlens[1:])
+    else:
+        _check_on(cu_seqlens, "cu_seqlens", dev)
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 \
+                or not cu_seqlens.is_contiguous() or cu_seqlens.numel() != sl.numel() + 1:
+            raise ValueError("cu_seqlens must be a contiguous int32 GPU tensor [B + 1]")
     out_k = torch.empty((count, total_tokens, H, D), dtype=kv_cache.dtype, device=kv_cache.device)
     out_v = torch.empty_like(out_k)
     if total_tokens == 0:
@@ -144,6 +172,16 @@ def gather_tokens(kv_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: 
     return out_k, out_v
 
 
+def _gpu(device) -> torch.device:
+    """``device`` as a GPU device with an index (None: the current GPU)."""
+    if device is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise ValueError(f"the attention workspace lives on a GPU, not on {dev}")
+    return dev if dev.index is not None else torch.device("cuda", torch.cuda.current_device())
+
+
 def attention_workspace_bytes(batch: int, n_q_heads: int, n_kv_heads: int, head_dim: int,
                               max_seq_len: int, dtype: torch.dtype = torch.bfloat16,
                               n_workgroups: int = 0, device=None) -> int:
@@ -151,7 +189,7 @@ def attention_workspace_bytes(batch: int, n_q_heads: int, n_kv_heads: int, head_
     (the default workgroup count depends on the device)."""
     if dtype not in _DTYPES:
         raise ValueError("dtype must be bfloat16 or float16")
-    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    dev = _gpu(device)
     with torch.cuda.device(dev):
         n = _lib.load().aegkv_paged_decode_attention_workspace_size(
             batch, n_q_heads, n_kv_heads, head_dim, max_seq_len, _DTYPES[dtype], n_workgroups)
@@ -166,11 +204,12 @@ def attention_workspace(batch: int, n_q_heads: int, n_kv_heads: int, head_dim: i
     """A device workspace large enough for every call of these sizes (None
     when the call needs none); reusable by consecutive calls on one stream,
     calls that may overlap (other streams) need their own."""
+    dev = _gpu(device)
     n = attention_workspace_bytes(batch, n_q_heads, n_kv_heads, head_dim, max_seq_len, dtype,
-                                  n_workgroups, device)
+                                  n_workgroups, dev)
     if n == 0:
         return None
-    return torch.empty(n, dtype=torch.uint8, device=device)
+    return torch.empty(n, dtype=torch.uint8, device=dev)
 
 
 # Workspaces kept per (device, stream) for calls that bring none.
@@ -202,8 +241,10 @@ class DecodePlan:
 
     def __init__(self, block_tables: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int,
                  n_kv_heads: int, n_workgroups: int = 0):
-        if not block_tables.is_cuda or not seq_lens.is_cuda or block_tables.dim() != 2:
-            raise ValueError("block_tables [B, max_blocks] and seq_lens [B] must be GPU tensors")
+        if not block_tables.is_cuda or not seq_lens.is_cuda or block_tables.dim() != 2 \
+                or block_tables.device != seq_lens.device:
+            raise ValueError("block_tables [B, max_blocks] and seq_lens [B] must be tensors on "
+                             "one GPU")
         self.block_tables = _int32_dense(block_tables)
         self.seq_lens = _int32_dense(seq_lens)
         self.batch = int(self.seq_lens.numel())
@@ -221,11 +262,25 @@ class DecodePlan:
                 _lib.check(int(n), "decode_plan")
             self.buffer = torch.empty(max(int(n), 1), dtype=torch.uint8, device=dev)
             self.nbytes = int(n)
+            stream = torch.cuda.current_stream(dev)
             rc = lib.aegkv_paged_decode_plan(
                 self.block_tables.data_ptr(), self.block_tables.size(1), self.seq_lens.data_ptr(),
                 self.batch, self.max_seq_len, self.n_kv_heads, self.n_workgroups,
-                self.buffer.data_ptr(), self.nbytes, torch.cuda.current_stream(dev).cuda_stream)
-        _lib.check(rc, "decode_plan")
+                self.buffer.data_ptr(), self.nbytes, stream.cuda_stream)
+            _lib.check(rc, "decode_plan")
+            # Calls on another stream wait for the build (wait_for_build).
+            self.stream = stream
+            self.built = torch.cuda.Event()
+            self.built.record(stream)
+
+    def wait_for_build(self, stream: torch.cuda.Stream) -> None:
+        """Order ``stream`` after the plan's build (a no-op on the build stream);
+        the plan's memory is then also kept from reuse until ``stream`` is done
+        with it."""
+        if stream != self.stream:
+            stream.wait_event(self.built)
+            for t in (self.buffer, self.block_tables, self.seq_lens):
+                t.record_stream(stream)
 
 
 def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
@@ -258,6 +313,16 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
         raise ValueError("q must be a GPU tensor [B, Hq, D] with dense heads")
     _check_cache_view(key_cache, "key_cache")
     _check_cache_view(value_cache, "value_cache")
+    dev = q.device
+    _check_on(key_cache, "key_cache", dev)
+    _check_on(value_cache, "value_cache", dev)
+    if block_tables is None or seq_lens is None:
+        raise ValueError("block_tables and seq_lens are required without a plan")
+    _check_on(block_tables, "block_tables", dev)
+    _check_on(seq_lens, "seq_lens", dev)
+    if block_tables.dim() != 2 or seq_lens.dim() != 1 or block_tables.size(0) != q.size(0) \
+            or seq_lens.numel() != q.size(0):
+        raise ValueError("block_tables must be [B, max_blocks] and seq_lens [B] for q's batch")
     if key_cache.stride(0) != value_cache.stride(0):
         raise ValueError("key_cache and value_cache must share the block stride")
     if q.dtype not in _DTYPES or key_cache.dtype != q.dtype or value_cache.dtype != q.dtype:
@@ -270,15 +335,23 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
         out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     elif out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D:
         raise ValueError("out must be [B, Hq, D] with dense heads")
+    elif out.dtype != q.dtype:
+        raise ValueError("out must have q's dtype")
+    else:
+        _check_on(out, "out", dev)
     if B == 0:
         return out
     ws_bytes = attention_workspace_bytes(B, Hq, Hkv, D, max_seq_len, q.dtype, n_workgroups,
                                          q.device)
     if ws_bytes > 0 and workspace is None:
         workspace = _cached_workspace(q.device, _stream(q), ws_bytes)
-    if ws_bytes > 0 and workspace.numel() * workspace.element_size() < ws_bytes:
-        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, "
-                         f"the call needs {ws_bytes}")
+    if ws_bytes > 0:
+        _check_on(workspace, "workspace", dev)
+        if workspace.numel() * workspace.element_size() < ws_bytes:
+            raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} "
+                             f"bytes, the call needs {ws_bytes}")
+    if plan is not None:
+        plan.wait_for_build(torch.cuda.current_stream(dev))
     ws_ptr = workspace.data_ptr() if (workspace is not None and ws_bytes > 0) else None
     with torch.cuda.device(q.device):
         if plan is not None:

@@ -31,6 +31,12 @@ constexpr int kCopyUnroll = 4;
 constexpr uint64_t kTileBytes = (uint64_t)kCopyThreads * 16 * kCopyUnroll;  // 16 KiB
 constexpr int kCopyWorkgroupsPerCu = 32;  // measured best of 2..32 with chunks 1..64 tiles
 constexpr int kCopyChunkTiles = 1;  // 0 = one contiguous range per workgroup
+// Largest grid of the per-tile (scatter) launch: HIP bounds a launch to
+// 2^32 - 1 work-items per dimension; beyond this many tiles the kernel's
+// round-robin loop deals the rest to the same workgroups.
+constexpr uint64_t kMaxCopyGrid = 1ull << 23;
+static_assert(kMaxCopyGrid * kCopyThreads <= 0xFFFFFFFFull,
+              "the per-tile copy grid must fit one launch dimension");
 
 // SRC_IDS / DST_IDS: whether the side is addressed through an id list (else
 // block i of the side is slot i).  Every memory access of the loop is issued
@@ -98,7 +104,7 @@ int launch_copy_blocks(const DeviceState* ds, const void* src, void* dst,
   // workgroup).
   const bool per_tile = !src_ids_dev && dst_ids_dev;
   const uint64_t max_grid =
-      per_tile ? (1ull << 30) : (uint64_t)std::max(ds->num_cu, 1) * kCopyWorkgroupsPerCu;
+      per_tile ? kMaxCopyGrid : (uint64_t)std::max(ds->num_cu, 1) * kCopyWorkgroupsPerCu;
   const uint64_t chunk = kCopyChunkTiles > 0 ? (uint64_t)kCopyChunkTiles
                                              : (n_tiles + max_grid - 1) / max_grid;
   const uint64_t n_chunks = (n_tiles + chunk - 1) / chunk;

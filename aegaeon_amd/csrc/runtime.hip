@@ -126,8 +126,18 @@ int ring_commit(DeviceState* ds, hipStream_t stream, size_t begin, size_t n) {
   hipError_t e = hipEventRecord(ev, stream);
   if (e != hipSuccess) {
     ds->spare_events.push_back(ev);
-    // The slice may still be read by the enqueued work: wait for the stream.
-    hipStreamSynchronize(stream);
+    // The slice may still be read by the enqueued work: wait for the stream
+    // before the ring can hand the slice out again.  If the wait fails too,
+    // nothing proves the device is done with the ring, so it is abandoned
+    // (left allocated, never reused); the next call grows a fresh one.
+    if (hipStreamSynchronize(stream) != hipSuccess) {
+      for (const auto& s : ds->inflight) ds->spare_events.push_back(s.ev);
+      ds->inflight.clear();
+      ds->host_ring = nullptr;
+      ds->dev_ring = nullptr;
+      ds->cap = 0;
+      ds->head = 0;
+    }
     return (int)e;
   }
   ds->inflight.push_back({begin, begin + n, ev});

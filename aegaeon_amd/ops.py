@@ -3,10 +3,11 @@
 ``swap`` is a drop-in for ``aegaeon.ops.swap`` (aegaeon/ops/ops.cpp:4-5,
 aegaeon/ops/swap.cu:25-59): same arguments, same meaning, the work is enqueued
 on the *current* torch stream (swap.cu:32) and nothing is returned.  It differs
-in three documented ways: the bytes per block come from the tensor's element
+in four documented ways: the bytes per block come from the tensor's element
 size instead of a hard-coded 2 (identical for the fp16/bf16 caches the
-reference uses), ids are range-checked and duplicate destination ids raise
-instead of silently racing.  Errors raise :class:`AegkvError`, the analogue of
+reference uses), ids are range-checked, duplicate destination ids raise
+instead of silently racing, and a swap space that is not pinned raises instead
+of silently copying synchronously.  Errors raise :class:`AegkvError`, the analogue of
 the reference's ``CUDART_CHECK`` (aegaeon/aegaeon/cuda_wrapper.py:152-155).
 
 PyTorch owns every buffer; the HIP kernels run through the C ABI of
@@ -54,9 +55,11 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _require_device(t: torch.Tensor, name: str) -> None:
+def _require_device(t: torch.Tensor, name: str, device: Optional[torch.device] = None) -> None:
     if not t.is_cuda:
         raise ValueError(f"{name} must be a GPU tensor")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} lives on {t.device}, the call on {device}")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
 
@@ -89,15 +92,20 @@ def swap(source_block_ids: IdList, target_block_ids: IdList, is_swap_in: bool,
     the GPU cache and the pinned CPU swap space, CPU->GPU when ``is_swap_in``.
 
     ``kv_cache``: contiguous GPU tensor ``[N_gpu, *block_shape]``;
-    ``kv_swap``: contiguous CPU tensor (pinned for an asynchronous copy)
-    ``[N_cpu, *block_shape]`` or flat.  ``staging``: "auto" packs scattered GPU
-    blocks through a per-stream device buffer so that each run of consecutive
-    CPU ids is a single DMA; None issues one DMA per run of consecutive id
-    pairs; a GPU uint8 tensor is used as the staging buffer directly.
+    ``kv_swap``: contiguous pinned CPU tensor ``[N_cpu, *block_shape]`` or
+    flat (the reference pins its swap space, worker.py:130-147; a pageable
+    tensor would turn every DMA into a blocking copy, so it is rejected).
+    ``staging``: "auto" packs scattered GPU blocks through a per-stream device
+    buffer so that each run of consecutive CPU ids is a single DMA; None issues
+    one DMA per run of consecutive id pairs; a GPU uint8 tensor is used as the
+    staging buffer directly.
     """
     _require_device(kv_cache, "kv_cache")
     if kv_swap.is_cuda or not kv_swap.is_contiguous():
         raise ValueError("kv_swap must be a contiguous CPU tensor")
+    if not kv_swap.is_pinned():
+        raise ValueError("kv_swap must be pinned host memory (torch pin_memory / hipHostMalloc): "
+                         "a pageable swap space makes every copy synchronous")
     src, n = _ids(source_block_ids)
     dst, n2 = _ids(target_block_ids)
     if n != n2:
@@ -116,6 +124,8 @@ def swap(source_block_ids: IdList, target_block_ids: IdList, is_swap_in: bool,
             stg = _staging_for(device, stream, bb)
         else:
             stg = staging
+            if stg is not None and (not stg.is_cuda or stg.device != device):
+                raise ValueError(f"staging must be a GPU tensor on {device}")
         stg_ptr, stg_bytes = (None, 0) if stg is None else (stg.data_ptr(), stg.numel() * stg.element_size())
         rc = _lib.load().aegkv_swap_blocks(
             _ptr(src), _ptr(dst), n, 1 if is_swap_in else 0, kv_cache.data_ptr(), n_dev,
@@ -128,7 +138,7 @@ def copy_blocks(src_pool: torch.Tensor, dst_pool: torch.Tensor, src_ids: Optiona
     """``dst_pool[dst_ids[i]] <- src_pool[src_ids[i]]`` on the GPU (None ids
     = identity).  Same-pool moves require disjoint src/dst sets."""
     _require_device(src_pool, "src_pool")
-    _require_device(dst_pool, "dst_pool")
+    _require_device(dst_pool, "dst_pool", src_pool.device)
     bb = block_bytes or block_bytes_of(src_pool)
     s, ns = _ids(src_ids)
     d, nd = _ids(dst_ids)
@@ -154,7 +164,7 @@ def pack_blocks(pool: torch.Tensor, ids: IdList, out: Optional[torch.Tensor] = N
             out = torch.empty((n, *pool.shape[1:]), dtype=pool.dtype, device=pool.device)
         else:
             out = torch.empty(n * bb, dtype=torch.uint8, device=pool.device)
-    _require_device(out, "out")
+    _require_device(out, "out", pool.device)
     if out.numel() * out.element_size() < n * bb:
         raise ValueError("out is smaller than the packed blocks")
     with torch.cuda.device(pool.device):
@@ -168,7 +178,7 @@ def scatter_blocks(staging: torch.Tensor, ids: IdList, pool: torch.Tensor,
                    block_bytes: Optional[int] = None) -> None:
     """``pool[ids[i]] <- staging[i]``."""
     _require_device(pool, "pool")
-    _require_device(staging, "staging")
+    _require_device(staging, "staging", pool.device)
     bb = block_bytes or block_bytes_of(pool)
     a, n = _ids(ids)
     if staging.numel() * staging.element_size() < n * bb:

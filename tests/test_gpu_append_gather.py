@@ -200,3 +200,48 @@ def test_gather_clips_capacity_bad_ids_and_long_lengths(device):
     for out, ref in ((gk, rk[0]), (gv, rv[0])):
         assert np.array_equal(out[want_rows], ref[src_rows])
         assert (out[36:52] == sentinel).all()           # the bad block's 16 tokens
+
+
+def test_gather_explicit_cu_seqlens(device):
+    """A caller's cu_seqlens places each sequence's rows (here with gaps and
+    out of order); rows no sequence covers keep their contents."""
+    rng = np.random.default_rng(34)
+    N, L, H, D = 48, 2, 2, 64
+    bits = random_bits(rng, (N, L, 2, 16, H, D), "bf16")
+    cache = to_device_bits(bits, "bf16", device)
+    lens = np.asarray([20, 5, 33], dtype=np.int64)
+    tables = _tables_for(rng, lens, N)
+    bt = torch.from_numpy(ko.pad_block_tables(tables)).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    starts = [70, 3, 30]                              # gaps 0..2, 8..29, 63..69
+    cu = torch.tensor(starts + [120], dtype=torch.int32, device=device)
+    out_k, out_v = A.gather_tokens(cache, bt, sl, 120, int(lens.max()), cu_seqlens=cu)
+    rk, rv = ko.gather_tokens(bits, tables, lens)     # packed in sequence order
+    packed = np.concatenate([[0], np.cumsum(lens)])
+    gk, gv = to_bits(out_k), to_bits(out_v)
+    for b, s in enumerate(starts):
+        n = int(lens[b])
+        assert np.array_equal(gk[:, s:s + n], rk[:, packed[b]:packed[b] + n]), b
+        assert np.array_equal(gv[:, s:s + n], rv[:, packed[b]:packed[b] + n]), b
+
+
+def test_gather_rejects_bad_metadata(device):
+    """cu_seqlens of another dtype, length or device, and tables or lengths on
+    the host, raise before any launch."""
+    rng = np.random.default_rng(35)
+    N, L, H, D = 16, 1, 2, 64
+    cache = to_device_bits(random_bits(rng, (N, L, 2, 16, H, D), "bf16"), "bf16", device)
+    lens = np.asarray([20, 5], dtype=np.int64)
+    bt = torch.from_numpy(ko.pad_block_tables(_tables_for(rng, lens, N))).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    good = torch.tensor([0, 20, 25], dtype=torch.int32, device=device)
+    for cu in (good.to(torch.int64), good[:2], good.cpu(), torch.cumsum(sl, 0)):
+        with pytest.raises(ValueError):
+            A.gather_tokens(cache, bt, sl, 25, 20, cu_seqlens=cu)
+    with pytest.raises(ValueError):
+        A.gather_tokens(cache, bt.cpu(), sl, 25, 20)
+    with pytest.raises(ValueError):
+        A.gather_tokens(cache, bt, sl.cpu(), 25, 20)
+    k, v = A.gather_tokens(cache, bt, sl, 25, 20, cu_seqlens=good)
+    torch.cuda.synchronize()
+    assert k.shape == (1, 25, H, D)

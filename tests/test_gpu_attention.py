@@ -374,3 +374,57 @@ def test_yi_decode_after_unified_pool_defrag(device):
     _check(to_bits(out), ref, "bf16")
     del pool, typed, view
     torch.cuda.empty_cache()
+
+
+def test_bad_inputs_raise_before_launch(device):
+    """Host-side checks: every tensor the kernels read or write must be on the
+    call's GPU, with the dtype the ABI reads it as; a host pointer never
+    reaches a kernel."""
+    lens = [40, 7]
+    _, _, _, _, _, q, kc, vc, bt, sl = _device_case(device, lens, 8, 2, 64, "bf16", 4)
+    ws = A.attention_workspace(2, 8, 2, 64, 40, torch.bfloat16)   # default device: the GPU
+    assert ws is not None and ws.is_cuda and ws.device == device
+    ok = A.paged_decode_attention(q, kc, vc, bt, sl, 0.125, 40, workspace=ws)
+    torch.cuda.synchronize()
+    cases = {
+        "cpu workspace": dict(workspace=torch.empty(ws.numel(), dtype=torch.uint8)),
+        "cpu block_tables": dict(block_tables=bt.cpu()),
+        "cpu seq_lens": dict(seq_lens=sl.cpu()),
+        "out of another dtype": dict(out=torch.empty(q.shape, dtype=torch.float16,
+                                                     device=device)),
+        "cpu out": dict(out=torch.empty(q.shape, dtype=q.dtype)),
+        "tables of another batch": dict(block_tables=bt[:1]),
+    }
+    for name, kw in cases.items():
+        args = dict(block_tables=bt, seq_lens=sl, workspace=ws)
+        args.update(kw)
+        with pytest.raises(ValueError):
+            A.paged_decode_attention(q, kc, vc, args.pop("block_tables"), args.pop("seq_lens"),
+                                     0.125, 40, **args)
+        torch.cuda.synchronize()
+    with pytest.raises(ValueError):
+        A.attention_workspace(2, 8, 2, 64, 40, torch.bfloat16, device="cpu")
+    again = A.paged_decode_attention(q, kc, vc, bt, sl, 0.125, 40, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(again, ok)
+
+
+def test_plan_built_on_another_stream(device):
+    """A plan built on one stream and used on another: the call's stream waits
+    for the build (the plan kernel is held back behind a spin on its stream,
+    so without the wait the attention would read an unwritten plan)."""
+    lens = [300, 1, 4000, 77, 0, 1500, 16, 2049]
+    lens, padded, q_b, kc_b, vc_b, q, kc, vc, bt, sl = _device_case(device, lens, 28, 4, 128,
+                                                                  "bf16", 41)
+    ref = A.paged_decode_attention(q, kc, vc, bt, sl, 1 / math.sqrt(128), 4000)
+    torch.cuda.synchronize()
+    build, use = torch.cuda.Stream(device=device), torch.cuda.Stream(device=device)
+    for trial in range(3):
+        with torch.cuda.stream(build):
+            torch.cuda._sleep(20_000_000)           # tens of ms on the build stream
+            plan = A.DecodePlan(bt, sl, 4000, 4)
+        with torch.cuda.stream(use):
+            got = A.paged_decode_attention(q, kc, vc, None, None, 1 / math.sqrt(128), 4000,
+                                           plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), trial

@@ -276,3 +276,19 @@ def test_swap_round_trip_property(device, case):
     assert np.array_equal(got[back], bits[src])
     untouched = np.setdiff1d(np.arange(n_pool), back)
     assert np.array_equal(got[untouched], bits[untouched])
+
+
+def test_swap_rejects_pageable_or_foreign_buffers(device):
+    """A pageable swap space (every DMA would block) and staging on the host
+    raise before anything is enqueued; the pool is untouched."""
+    cache = torch.zeros((4, 2, 16, 1, 64), dtype=torch.float16, device=device)
+    pageable = torch.zeros((4, 2, 16, 1, 64), dtype=torch.float16)
+    with pytest.raises(ValueError):
+        ops.swap([0, 1], [2, 3], False, cache, pageable)
+    pinned = torch.zeros_like(pageable).pin_memory()
+    with pytest.raises(ValueError):
+        ops.swap([0, 1], [2, 3], False, cache, pinned, staging=torch.empty(1 << 16,
+                                                                           dtype=torch.uint8))
+    ops.swap([0, 1], [2, 3], False, cache, pinned)
+    torch.cuda.synchronize()
+    assert torch.equal(pinned[2:], cache[:2].cpu())
