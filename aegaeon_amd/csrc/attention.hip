@@ -51,6 +51,8 @@
 // K/V in flight while one is computed.
 #include <algorithm>
 #include <cmath>
+#include <map>
+#include <mutex>
 #include <utility>
 
 #include "aegkv_internal.h"
@@ -1128,12 +1130,66 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
   }
   return AEGKV_OK;
 }
+// Workspace of aegkv_paged_decode_attention_noalloc, held by the library in
+// device memory it never allocates: the merge descriptors and fp32 partials of
+// one call (the same layout the caller's workspace holds).  Every GPU the
+// library runs on has its own copy of the array until the process ends; its
+// address there comes from hipGetSymbolAddress, once per device.  Nothing in
+// it needs clearing between calls: every byte a call's combine reads is
+// written by the same call.
+constexpr uint64_t kScratchBytes = 32ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_ptr;  // device -> address of `scratch` on it
+
+// Address of the current device's `scratch` (looked up on the first call on a
+// device, with that device current).
+int scratch_of_current_device(void** ptr) {
+  int dev = 0;
+  AEGKV_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it != g_scratch_ptr.end()) {
+    *ptr = it->second;
+    return AEGKV_OK;
+  }
+  void* p = nullptr;
+  AEGKV_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  g_scratch_ptr[dev] = p;
+  *ptr = p;
+  return AEGKV_OK;
+}
 }  // namespace
 }  // namespace aegkv
 
 using namespace aegkv;
 
 extern "C" {
+
+int aegkv_paged_decode_attention_noalloc(void* out, int64_t out_batch_stride, const void* q,
+                                         int64_t q_batch_stride, const void* key_cache,
+                                         const void* value_cache, int64_t cache_block_stride,
+                                         int64_t n_blocks, const int32_t* block_tables,
+                                         int32_t max_blocks, const int32_t* seq_lens,
+                                         int32_t batch, int32_t max_seq_len, int32_t n_q_heads,
+                                         int32_t n_kv_heads, int32_t head_dim,
+                                         int32_t block_size, float scale, int32_t dtype,
+                                         int32_t n_workgroups, aegkv_stream_t stream) {
+  const int64_t need = aegkv_paged_decode_attention_workspace_size(
+      batch, n_q_heads, n_kv_heads, head_dim, max_seq_len, dtype, n_workgroups);
+  if (need < 0) return (int)need;
+  if ((uint64_t)need > kScratchBytes) return AEGKV_ERR_SCRATCH;
+  if (batch == 0) return AEGKV_OK;
+  if (!block_tables) return AEGKV_ERR_INVALID_ARG;
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  return run_attention(out, out_batch_stride, q, q_batch_stride, key_cache, value_cache,
+                       cache_block_stride, n_blocks, block_tables, max_blocks, nullptr, 0,
+                       seq_lens, batch, max_seq_len, n_q_heads, n_kv_heads, head_dim,
+                       block_size, scale, dtype, n_workgroups, ws, kScratchBytes, stream);
+}
 
 int64_t aegkv_paged_decode_attention_workspace_size(int32_t batch, int32_t n_q_heads,
                                                      int32_t n_kv_heads, int32_t head_dim,

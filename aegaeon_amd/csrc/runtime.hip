@@ -161,6 +161,7 @@ const char* aegkv_strerror(int code) {
     case AEGKV_ERR_RUNTIME: return "aegkv: a HIP runtime query failed while sizing the call";
     case AEGKV_ERR_NO_SPACE: return "aegkv: not enough free blocks after reclaiming moves";
     case AEGKV_ERR_IN_USE: return "aegkv: request lives elsewhere, or the space still holds requests";
+    case AEGKV_ERR_SCRATCH: return "aegkv: the call needs a larger workspace than the 32 MiB the no-allocation entry point holds";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);

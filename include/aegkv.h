@@ -198,6 +198,31 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
                                  int32_t n_workgroups, void* workspace,
                                  uint64_t workspace_bytes, aegkv_stream_t stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): aegkv_paged_decode_attention with the same arguments
+ * minus the workspace, which here is a 32 MiB array of device memory the
+ * library holds per GPU (a file-scope __device__ array, one copy per device
+ * until the process ends).  The call allocates nothing.  Calls whose
+ * workspace_size exceeds 32 MiB return AEGKV_ERR_SCRATCH before anything is
+ * enqueued (with one workgroup per CU, the Qwen2.5-7B shape, 28/4 heads at
+ * D 128, fits every batch, and Llama-2-13B's 40/40 up to 1500 sequences; see
+ * aegkv_paged_decode_attention_workspace_size).  Every call on a GPU uses
+ * that GPU's one array: calls
+ * that may overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller.  Results equal aegkv_paged_decode_attention's bit
+ * for bit. */
+#define AEGKV_ERR_SCRATCH (-11)      /* call needs more than the no-alloc scratch */
+int aegkv_paged_decode_attention_noalloc(void* out, int64_t out_batch_stride, const void* q,
+                                         int64_t q_batch_stride, const void* key_cache,
+                                         const void* value_cache, int64_t cache_block_stride,
+                                         int64_t n_blocks, const int32_t* block_tables,
+                                         int32_t max_blocks, const int32_t* seq_lens,
+                                         int32_t batch, int32_t max_seq_len, int32_t n_q_heads,
+                                         int32_t n_kv_heads, int32_t head_dim,
+                                         int32_t block_size, float scale, int32_t dtype,
+                                         int32_t n_workgroups, aegkv_stream_t stream);
+
 /* Decode plan: the work split of aegkv_paged_decode_attention for one batch
  * of block tables and lengths, built once per decode step and shared by every
  * layer's call (the layers of a step attend over the same tables, as the
