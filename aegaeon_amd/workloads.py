@@ -307,3 +307,24 @@ def unified_pool_workload(seed: int = 0, slab_bytes: int = 1 << 30) -> UnifiedPo
         live = rng.permutation(valid)[:total]
         wl.tables[name] = split_tables(live, need)
     return wl
+
+
+def pinnable_blocks(block_bytes: int, want: int, reserve: int = 32 << 30) -> int:
+    """How many blocks of ``block_bytes`` a pinned host pool on this host may
+    hold, up to ``want``: torch's pinned allocator rounds a request up to a
+    power of two, and the pool takes at most half of MemAvailable less
+    ``reserve``.  Halves ``want`` until it fits (0 when nothing does)."""
+    avail = 0
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemAvailable:"):
+                    avail = int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    budget = (avail - reserve) // 2
+    n = want
+    while n > 0 and (1 << (n * block_bytes - 1).bit_length()) > budget:
+        n //= 2
+    return n
+

@@ -428,3 +428,87 @@ def test_plan_built_on_another_stream(device):
                                            plan=plan)
         torch.cuda.synchronize()
         assert torch.equal(got, ref), trial
+
+
+def test_yi_decode_step_after_unified_pool_defrag(device):
+    """The whole decode step of the unified-pool workload at full size: after
+    the Yi-1.5-9B compaction, one token per sequence is appended to every one
+    of the 48 layers of the compacted pool (slots through the rewritten
+    tables, worker.py:628-633), then attention over ctx + 1 tokens runs for
+    layers 0 and 47 through a plan over the rewritten tables.  The pool after
+    the append equals the pool before it with the oracle's append applied to
+    the touched blocks (bit for bit, so nothing else changed), and attention
+    matches the float64 oracle on the K/V taken before the moves plus the
+    appended token."""
+    from aegaeon_amd import ops
+    from aegaeon_amd.pool import plan_compaction, remap_tables
+    from aegaeon_amd.workloads import unified_pool_workload
+    wl = unified_pool_workload(0)
+    g = wl.geometries[wl.decode_model]
+    bb = g.block_bytes
+    torch.cuda.empty_cache()
+    if torch.cuda.get_device_properties(device).total_memory < 2 * wl.pool_bytes + (16 << 30):
+        pytest.skip("needs %d GiB of device memory" % ((2 * wl.pool_bytes >> 30) + 16))
+    gen = torch.Generator(device=device).manual_seed(9)
+    pool = torch.empty(wl.pool_bytes, dtype=torch.uint8, device=device)
+    pool.view(torch.bfloat16).normal_(generator=gen)
+    nb = wl.pool_bytes // bb
+    typed = pool[:nb * bb].view(torch.bfloat16).view(nb, *g.block_shape)
+    old_tables = wl.tables[wl.decode_model]
+    used = sorted({b for t in old_tables for b in t})
+    pos = {b: i for i, b in enumerate(used)}
+    idx = torch.tensor(used, device=device)
+    layers = (0, g.n_layers - 1)
+    kv_before = {l: (to_bits(typed[idx, l, 0]), to_bits(typed[idx, l, 1])) for l in layers}
+    src, dst = plan_compaction([b for t in old_tables for b in t],
+                               wl.valid_ids(wl.decode_model))
+    ops.defrag_blocks(pool, src, dst, block_bytes=bb)
+    tables = remap_tables(old_tables, src, dst)
+    ctx = np.asarray(wl.yi_context_lens, dtype=np.int64)
+    B = len(ctx)
+    # the append: one token per sequence and layer at position ctx
+    key = torch.randn((g.n_layers, B, g.n_kv_heads, g.head_dim), generator=gen,
+                      device=device).to(torch.bfloat16)
+    val = torch.randn(key.shape, generator=gen, device=device).to(torch.bfloat16)
+    slots = ko.slot_mapping(tables, ctx, [c + 1 for c in ctx])
+    targets = sorted({int(s) // 16 for s in slots})
+    tidx = torch.tensor(targets, device=device)
+    snapshot = pool.clone()
+    expect = to_bits(typed[tidx])                       # [n_target, L, 2, 16, Hkv, D]
+    tpos = {b: i for i, b in enumerate(targets)}
+    compact_slots = np.asarray([tpos[int(s) // 16] * 16 + int(s) % 16 for s in slots],
+                               dtype=np.int64)
+    ko.append_layers(to_bits(key), to_bits(val), expect, compact_slots)
+    A.append_kv(key, val, typed, torch.from_numpy(slots).to(device))
+    torch.cuda.synchronize()
+    snap_typed = snapshot[:nb * bb].view(torch.bfloat16).view(nb, *g.block_shape)
+    snap_typed[tidx] = to_device_bits(expect, "bf16", device)
+    assert torch.equal(pool, snapshot)                  # the append and nothing else
+    del snapshot, snap_typed
+    # attention over ctx + 1 through the rewritten tables, one plan for the step
+    lens = ctx + 1
+    view = typed.permute(1, 2, 0, 3, 4, 5)
+    bt = torch.from_numpy(ko.pad_block_tables(tables)).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    ml = int(lens.max())
+    scale = 1 / math.sqrt(g.head_dim)
+    plan = A.DecodePlan(bt, sl, ml, g.n_kv_heads)
+    compact = ko.pad_block_tables([[pos[b] for b in t] for t in old_tables])
+    kb, vb = to_bits(key), to_bits(val)
+    for l in layers:
+        q = torch.randn((B, g.n_q_heads, g.head_dim), generator=gen,
+                        device=device).to(torch.bfloat16)
+        out = A.paged_decode_attention(q, view[l, 0], view[l, 1], None, None, scale, ml,
+                                       plan=plan)
+        torch.cuda.synchronize()
+        k_ref, v_ref = (x.copy() for x in kv_before[l])
+        for b in range(B):                               # the appended token, pre-move ids
+            blk = pos[old_tables[b][int(ctx[b]) // 16]]
+            k_ref[blk, int(ctx[b]) % 16] = kb[l, b]
+            v_ref[blk, int(ctx[b]) % 16] = vb[l, b]
+        ref = ko.paged_decode_attention(ko.bits_to_float(to_bits(q), "bf16"),
+                                        ko.bits_to_float(k_ref, "bf16"),
+                                        ko.bits_to_float(v_ref, "bf16"), compact, lens, scale)
+        _check(to_bits(out), ref, "bf16")
+    del pool, typed, view
+    torch.cuda.empty_cache()

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from aegaeon_amd import ops
+from aegaeon_amd.workloads import pinnable_blocks
 from oracle import kv_oracle as ko
 from tests.kvtest_utils import load_golden, random_bits, to_bits, to_device_bits
 
@@ -292,3 +293,52 @@ def test_swap_rejects_pageable_or_foreign_buffers(device):
     ops.swap([0, 1], [2, 3], False, cache, pinned)
     torch.cuda.synchronize()
     assert torch.equal(pinned[2:], cache[:2].cpu())
+
+
+_LLAMA_BB = 40 * 2 * 16 * 40 * 128 * 2
+_N_HOST = pinnable_blocks(_LLAMA_BB, 4096)
+
+
+@pytest.mark.parametrize("n_host", [_N_HOST], ids=[f"{_N_HOST}of4096blocks"])
+def test_llama_swap_through_pinned_host(device, n_host):
+    """The Llama-2-13B swap as the worker runs it (worker.py:753-762): n_host
+    of the workload's 4096 scattered 12.5 MiB blocks (all of them when the
+    host can pin 64 GiB; the test id states the count) go out to a pinned host
+    pool through ops.swap (staged pack, one DMA per host run) and come back
+    through ops.swap into a disjoint seeded free set.  Checked bit for bit on
+    both sides: the host pool against the source blocks (read back with a
+    plain copy), the swapped-in blocks against the source blocks, and blocks
+    no move touched against a snapshot."""
+    if n_host == 0:
+        pytest.skip("the host cannot pin even one 12.5 MiB block")
+    from aegaeon_amd.workloads import llama_swap_workload
+    wl = llama_swap_workload(0)
+    bb = wl.geometry.block_bytes
+    assert bb == _LLAMA_BB
+    torch.cuda.empty_cache()
+    if torch.cuda.get_device_properties(device).total_memory < wl.n_pool_blocks * bb + (16 << 30):
+        pytest.skip("needs %d GiB of device memory" % ((wl.n_pool_blocks * bb >> 30) + 16))
+    pool = torch.empty((wl.n_pool_blocks, bb), dtype=torch.uint8, device=device)
+    pool.view(torch.int32).random_(generator=torch.Generator(device=device).manual_seed(8))
+    src = np.asarray(wl.gpu_ids[:n_host], dtype=np.int64)
+    dst = np.asarray(wl.swap_in_ids[:n_host], dtype=np.int64)
+    host_ids = np.asarray(wl.cpu_ids[:n_host], dtype=np.int64)
+    untouched = np.setdiff1d(np.arange(wl.n_pool_blocks), np.concatenate([src, dst]))
+    keep = torch.from_numpy(untouched[::max(1, len(untouched) // 64)][:64]).to(device)
+    before = pool[keep].clone()
+    host = torch.empty((n_host, bb), dtype=torch.uint8, pin_memory=True)
+    print(f"swap-out of {n_host} blocks ({n_host * bb / 2**30:.1f} GiB)", flush=True)
+    ops.swap(src, host_ids, False, pool, host)
+    ops.swap(host_ids, dst, True, pool, host)
+    torch.cuda.synchronize()
+    step = 128
+    for c in range(0, n_host, step):
+        s = torch.from_numpy(src[c:c + step]).to(device)
+        d = torch.from_numpy(dst[c:c + step]).to(device)
+        h = host[c:c + step].to(device)            # host rows c.. hold host ids c.. (a run)
+        assert torch.equal(h, pool[s]), c
+        assert torch.equal(pool[d], pool[s]), c
+    assert torch.equal(pool[keep], before)
+    del pool, host, before
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
