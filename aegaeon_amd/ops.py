@@ -136,7 +136,8 @@ def swap(source_block_ids: IdList, target_block_ids: IdList, is_swap_in: bool,
 def copy_blocks(src_pool: torch.Tensor, dst_pool: torch.Tensor, src_ids: Optional[IdList],
                 dst_ids: Optional[IdList], block_bytes: Optional[int] = None) -> None:
     """``dst_pool[dst_ids[i]] <- src_pool[src_ids[i]]`` on the GPU (None ids
-    = identity).  Same-pool moves require disjoint src/dst sets."""
+    = identity; with both None, every block of the smaller pool is copied and
+    no id list is uploaded).  Same-pool moves require disjoint src/dst sets."""
     _require_device(src_pool, "src_pool")
     _require_device(dst_pool, "dst_pool", src_pool.device)
     bb = block_bytes or block_bytes_of(src_pool)
@@ -144,7 +145,10 @@ def copy_blocks(src_pool: torch.Tensor, dst_pool: torch.Tensor, src_ids: Optiona
     d, nd = _ids(dst_ids)
     if s is not None and d is not None and ns != nd:
         raise ValueError("src_ids and dst_ids differ in length")
-    n = ns if s is not None else nd
+    if s is None and d is None:
+        n = min(_num_blocks(src_pool, bb), _num_blocks(dst_pool, bb))
+    else:
+        n = ns if s is not None else nd
     with torch.cuda.device(src_pool.device):
         rc = _lib.load().aegkv_copy_blocks(
             src_pool.data_ptr(), _num_blocks(src_pool, bb), dst_pool.data_ptr(),

@@ -25,16 +25,21 @@ torch.cuda.synchronize() brackets every timed region.
 Secondary lines (``ops``): the per-layer launch pattern of vLLM; paged decode
 attention (Qwen2.5-7B GQA 28/4, 128 sequences, lognormal mean 1500, up to 8192
 tokens) in us per layer; block pack and scatter for the Llama-2-13B swap
-workload (32 x 2048 tokens, 4096 blocks of 12.5 MiB) plus a sampled PCIe leg to
-pinned host; defrag of the unified multi-model pool followed by a Yi-1.5-9B
+workload (32 x 2048 tokens, 4096 blocks of 12.5 MiB) and the same swap through
+ops.swap out to pinned host memory and back (all 4096 blocks when the host can
+pin them), with its pack, DMA and scatter legs; defrag of the unified
+multi-model pool followed by a Yi-1.5-9B
 decode step (append + attention); token gather; a swap-out on a side stream
 overlapped with 28 layers of decode attention; the prefill side (prompt KV
 write and causal varlen attention, 4 x 2048 tokens); device-side input preparation
 against the reference's host loops; the block manager's host bookkeeping
-(native against the reference's algorithm, same block ids).
+(native against the reference's algorithm, same block ids); the copy floor,
+the block-copy kernel moving the headline append's bytes.
 
-The CPU baseline is the numpy oracle's append timed on the host on a bounded
-sample of the same workload.
+The CPU baseline is the reference's path restated with torch on the host
+(oracle/torch_cpu.py) on every core of the affinity mask, 3 warm-ups and the
+median of at least 10 runs: the same append into the full pool, plus one
+layer of the attention batch in float32 and the swap as host memcpy.
 """
 from __future__ import annotations
 
@@ -54,6 +59,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+PCIE_PEAK_GBS = 64.0   # PCIe 5.0 x16, one direction
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
 METRIC = "KV gather/append GB/s (%HBM peak); paged decode-attn µs/layer @Qwen2.5-7B"
 ROTATE_STEPS = 32
@@ -250,23 +256,68 @@ def bench_pack(args, timer):
     p_ms, _ = timer.run(pack, steps)
     s_ms, _ = timer.run(scatter, steps)
     nbytes = wl.pack_bytes()
-    # PCIe leg on a sample: D2H of packed blocks into pinned host, then H2D back
-    n_s = min(args.pcie_blocks, wl.n_blocks)
-    host = torch.empty((n_s, bb), dtype=torch.uint8, pin_memory=True)
-    torch.cuda.synchronize()
-    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    e[0].record()
-    host.copy_(staging[:n_s], non_blocking=True)
-    e[1].record()
-    staging[:n_s].copy_(host, non_blocking=True)
-    e[2].record()
-    torch.cuda.synchronize()
-    d2h = n_s * bb / (e[0].elapsed_time(e[1]) * 1e-3) / 1e9
-    h2d = n_s * bb / (e[1].elapsed_time(e[2]) * 1e-3) / 1e9
-    del pool, staging, host
+    swap = bench_swap_host(args, wl, pool, staging, src, dst) if args.swap_blocks != 0 else None
+    del pool, staging
     torch.cuda.empty_cache()
-    return {"wl": wl, "bytes": nbytes, "pack_ms": p_ms, "scatter_ms": s_ms,
-            "pcie_blocks": n_s, "d2h_gbs": d2h, "h2d_gbs": h2d}
+    return {"wl": wl, "bytes": nbytes, "pack_ms": p_ms, "scatter_ms": s_ms, "swap": swap}
+
+
+def bench_swap_host(args, wl, pool, staging, src, dst):
+    """The Llama-2-13B swap as the worker runs it (worker.py:753-762): n of
+    the 4096 scattered blocks out to a pinned host pool with ops.swap (staged:
+    pack into a 256 MiB device buffer, one DMA per run of host ids) and back
+    into the disjoint free set with ops.swap (DMA into staging, scatter).  n is
+    4096 when the host can pin the 50 GiB (64 GiB after torch's power-of-two
+    rounding), else the largest power-of-two fraction that fits; the line
+    states n.  The DMA legs alone are ops.swap of the contiguous staging
+    buffer (no pack: one DMA for all n blocks each way).  Each figure is the
+    median of 3 calls, timed with events on the calling stream."""
+    import torch
+    from aegaeon_amd import ops
+    from aegaeon_amd.workloads import pinnable_blocks
+    bb = wl.geometry.block_bytes
+    want = wl.n_blocks if args.swap_blocks < 0 else min(args.swap_blocks, wl.n_blocks)
+    n = pinnable_blocks(bb, want)
+    if n == 0:
+        return None
+    t0 = time.perf_counter()
+    host = torch.empty((n, bb), dtype=torch.uint8, pin_memory=True)
+    pin_s = time.perf_counter() - t0
+    host_ids = np.arange(n, dtype=np.int64)
+
+    def timed(fn, reps=3):
+        out = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1))
+        return sorted(out)[len(out) // 2]
+
+    res = {"blocks": n, "of_blocks": wl.n_blocks, "pin_s": pin_s}
+    res["swap_out_ms"] = timed(lambda: ops.swap(src[:n], host_ids, False, pool, host))
+    res["swap_in_ms"] = timed(lambda: ops.swap(host_ids, dst[:n], True, pool, host))
+    res["dma_d2h_ms"] = timed(lambda: ops.swap(host_ids, host_ids, False, staging[:n], host,
+                                               staging=None))
+    res["dma_h2d_ms"] = timed(lambda: ops.swap(host_ids, host_ids, True, staging[:n], host,
+                                               staging=None))
+    res["pack_ms"] = timed(lambda: ops.pack_blocks(pool, src[:n], out=staging[:n]))
+    res["scatter_ms"] = timed(lambda: ops.scatter_blocks(staging[:n], dst[:n], pool))
+    # the round trip is bit-exact (checked here on a sample; the tests check all)
+    k = torch.from_numpy(src[:min(n, 8)]).to(pool.device)
+    j = torch.from_numpy(dst[:min(n, 8)]).to(pool.device)
+    ops.swap(src[:n], host_ids, False, pool, host)
+    ops.swap(host_ids, dst[:n], True, pool, host)
+    torch.cuda.synchronize()
+    if not torch.equal(pool[k], pool[j]) or not torch.equal(host[:len(k)].to(pool.device),
+                                                             pool[k]):
+        raise RuntimeError("swap round trip is not bit-exact")
+    del host
+    torch._C._host_emptyCache()
+    return res
 
 
 # ------------------------------------------------------------- unified pool + defrag
@@ -662,37 +713,129 @@ def bench_calib(args, timer):
     return {"bytes": 2 * CALIB_BLOCKS * CALIB_BLOCK_BYTES, "ms": ms}
 
 
+# ------------------------------------------------------------------- copy floor
+FLOOR_BLOCKS, FLOOR_BLOCK_BYTES = 14, 1 << 20   # 14 MiB read + 14 MiB written = 29.36 MB
+
+
+def bench_copy_floor(args, timer):
+    """The copy floor at the headline append's bytes: the block-copy kernel
+    copying 14 contiguous 1 MiB blocks (14,680,064 B read, the same written:
+    29,360,128 B, the append's 29,362,176 B less its 2 KiB of slots) in its
+    identity form (no id list, so no upload ahead of the kernel), with sources
+    and destinations rotated over 32 regions (0.9 GB) as the append rotates
+    its steps, so neither side is served from the last-level cache."""
+    import torch
+    from aegaeon_amd import ops
+    dev = torch.device("cuda", 0)
+    R = ROTATE_STEPS
+    src = torch.ones((R, FLOOR_BLOCKS, FLOOR_BLOCK_BYTES), dtype=torch.uint8, device=dev)
+    outs = torch.empty((R, FLOOR_BLOCKS, FLOOR_BLOCK_BYTES), dtype=torch.uint8, device=dev)
+
+    def copy(i):
+        r = i % R
+        ops.copy_blocks(src[r], outs[r], None, None)
+
+    for i in range(R):
+        copy(i)
+    torch.cuda.synchronize()
+    ms, _ = timer.run(copy, args.steps)
+    if not torch.equal(outs[0], src[0]):
+        raise RuntimeError("copy floor: the copy is wrong")
+    del src, outs
+    torch.cuda.empty_cache()
+    return {"bytes": 2 * FLOOR_BLOCKS * FLOOR_BLOCK_BYTES, "ms": ms}
+
+
 # ---------------------------------------------------------------------- CPU baseline
-def cpu_baseline_append(args):
-    """The oracle's append (numpy, one thread) on a bounded sample: the same
-    256 tokens x 28 layers, into a compact pool holding only the touched
-    blocks; repeated for about --cpu-seconds."""
-    from aegaeon_amd.workloads import qwen_append_batch
-    from oracle import kv_oracle as ko
-    wb = qwen_append_batch(args.seed)
-    g = wb.geometry
-    slots = wb.slot_mapping()
-    blocks = np.unique(slots // 16)
-    remap = {int(b): i for i, b in enumerate(blocks)}
-    cslots = np.asarray([remap[int(s // 16)] * 16 + int(s % 16) for s in slots], dtype=np.int64)
-    storage = np.zeros((len(blocks), *g.block_shape), dtype=np.uint16)
-    rng = np.random.default_rng(args.seed)
-    key = rng.integers(0, 1 << 16, size=(g.n_layers, wb.batch, g.n_kv_heads, g.head_dim),
-                       dtype=np.uint16)
-    val = key[::-1].copy()
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        ko.append_layers(key, val, storage, cslots)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > args.cpu_seconds:
-            break
-    return {"value": round(wb.append_bytes() * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"numpy oracle append_layers on 1 host thread: {reps} repetitions of the "
-                      f"full 256-token x 28-layer Qwen2.5-7B append into a compact "
-                      f"{len(blocks)}-block pool in {el:.1f} s",
-            "cpu_model": _cpu_model()}
+def _median_time(fn, warmup=3, runs=10, min_s=1.0):
+    """3 warm-ups, then the median of at least ``runs`` timed calls (more
+    while under ``min_s`` seconds in total)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    t_end = time.perf_counter() + min_s
+    while len(ts) < runs or (time.perf_counter() < t_end and len(ts) < 1000):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts)
+
+
+def cpu_baseline(args):
+    """The reference's path restated with torch on the host CPU (the oracle's
+    torch_cpu module), timed in this process on every core of the affinity
+    mask: 3 warm-ups, then the median of at least 10 runs.  The headline
+    figure is the Qwen2.5-7B all-layer append into the full 19,014-block pool
+    (17.4 GB of host memory); ``ops`` holds one layer of the Qwen2.5-7B decode
+    attention (float32 from bf16, 128 sequences) and the Llama-2-13B swap as
+    host memcpy of 12.5 MiB blocks (a 64-block sample, as GB/s)."""
+    import torch
+    from aegaeon_amd.workloads import llama_swap_workload, qwen_append_batch, \
+        qwen_attention_batch, successive_step_slots
+    from oracle import torch_cpu as tc
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        gen = torch.Generator().manual_seed(args.seed)
+        wb = qwen_append_batch(args.seed)
+        g = wb.geometry
+        R = ROTATE_STEPS
+        storage = torch.empty((wb.n_pool_blocks, *g.block_shape), dtype=torch.bfloat16)
+        keys = torch.randn((R, g.n_layers, wb.batch, g.n_kv_heads, g.head_dim),
+                           generator=gen).to(torch.bfloat16)
+        vals = torch.randn(keys.shape, generator=gen).to(torch.bfloat16)
+        slots = torch.from_numpy(successive_step_slots(wb, R))
+        step = [0]
+
+        def app():
+            r = step[0] % R
+            step[0] += 1
+            tc.append_layers(keys[r], vals[r], storage, slots[r])
+
+        t_app, n_app = _median_time(app)
+        del storage, keys, vals
+        ab = qwen_attention_batch(args.seed)
+        ag = ab.geometry
+        kc = torch.randn((ab.n_pool_blocks, 16, ag.n_kv_heads, ag.head_dim),
+                         generator=gen).to(torch.bfloat16)
+        vc = torch.randn(kc.shape, generator=gen).to(torch.bfloat16)
+        q = torch.randn((ab.batch, ag.n_q_heads, ag.head_dim), generator=gen).to(torch.bfloat16)
+        bt = torch.from_numpy(ab.padded_tables())
+        sl = torch.from_numpy(ab.seq_lens)
+        scale = 1.0 / math.sqrt(ag.head_dim)
+        t_att, n_att = _median_time(lambda: tc.paged_decode_attention(q, kc, vc, bt, sl, scale))
+        del kc, vc
+        wl = llama_swap_workload(args.seed)
+        bb = wl.geometry.block_bytes
+        n_s = 64
+        src_pool = torch.ones((2 * n_s, bb), dtype=torch.uint8)
+        dst_pool = torch.zeros((n_s, bb), dtype=torch.uint8)
+        src_ids = np.random.default_rng(args.seed).permutation(2 * n_s)[:n_s]
+        t_swp, n_swp = _median_time(lambda: tc.swap_blocks(src_ids, range(n_s), src_pool,
+                                                           dst_pool))
+        del src_pool, dst_pool
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": round(wb.append_bytes() / t_app / 1e9, 3), "unit": "GB/s",
+            "cores": cores, "kind": "port",
+            "sample": f"torch CPU restatement of the append (oracle/torch_cpu.py) on {cores} "
+                      f"threads: the full 256-token x 28-layer Qwen2.5-7B append into the "
+                      f"{wb.n_pool_blocks}-block pool, {R} successive decode steps rotated as "
+                      f"on the GPU, median of {n_app} runs after 3 warm-ups "
+                      f"({t_app * 1e3:.2f} ms per step)",
+            "cpu_model": _cpu_model(),
+            "ops": {
+                "paged_decode_attention_fp32": {
+                    "workload": "one layer of the Qwen2.5-7B decode batch (128 seqs, "
+                                "sum len 189059), float32 from bf16",
+                    "us_per_layer": round(t_att * 1e6, 1),
+                    "GB/s": round(ab.attention_bytes() / t_att / 1e9, 3), "runs": n_att},
+                "swap_host_memcpy": {
+                    "workload": f"Llama-2-13B swap restated as host-to-host block copies, "
+                                f"{n_s} of the 4096 12.5 MiB blocks",
+                    "ms": round(t_swp * 1e3, 2),
+                    "GB/s": round(n_s * bb / t_swp / 1e9, 2), "runs": n_swp}}}
 
 
 def _cpu_model() -> str:
@@ -728,10 +871,12 @@ def main(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--swap-seqs", type=int, default=32)
-    p.add_argument("--pcie-blocks", type=int, default=64)
+    p.add_argument("--swap-blocks", type=int, default=-1,
+                   help="blocks of the Llama-2-13B swap sent through pinned host memory "
+                        "(-1 = all 4096 when the host can pin them; 0 = skip)")
     p.add_argument("--only", default="all",
                    help="comma list of append,attention,pack,defrag,gather,overlap,prefill,"
-                        "prepare,bm,calib or 'all'")
+                        "prepare,bm,calib,floor or 'all'")
     args = p.parse_args(argv)
     if args.gpus != 1:
         print(json.dumps({"error": "aegaeon_amd's KV data path is per-GPU and runs no "
@@ -748,7 +893,7 @@ def main(argv=None):
     log(f"device: {torch.cuda.get_device_name(0)}")
     only = set(args.only.split(",")) if args.only != "all" else \
         {"append", "attention", "pack", "defrag", "gather", "overlap", "prefill", "prepare", "bm",
-         "calib"}
+         "calib", "floor"}
     timer = Timer()
     log(f"spin calibration: {timer.cycles_per_ms:.0f} cycles/ms")
     res = {}
@@ -757,14 +902,14 @@ def main(argv=None):
                      ("overlap", bench_overlap), ("prefill", bench_prefill),
                      ("prepare", bench_prepare),
                      ("bm", bench_block_manager),
-                     ("calib", bench_calib)):
+                     ("calib", bench_calib), ("floor", bench_copy_floor)):
         if name in only:
             t0 = time.perf_counter()
             res[name] = fn(args, timer)
             log(f"{name} done in {time.perf_counter() - t0:.1f} s")
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_append(args)
+        cpu = cpu_baseline(args)
         log(f"cpu baseline done: {cpu['value']} GB/s")
 
     line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -821,8 +966,26 @@ def main(argv=None):
             "bytes": pk["bytes"], "pack_GB/s": round(pg, 1), "scatter_GB/s": round(sg, 1),
             "pack_frac_hbm": round(pg / HBM_PEAK_GBS, 4),
             "scatter_frac_hbm": round(sg / HBM_PEAK_GBS, 4),
-            "pcie_sample_blocks": pk["pcie_blocks"], "d2h_GB/s": round(pk["d2h_gbs"], 1),
-            "h2d_GB/s": round(pk["h2d_gbs"], 1)}
+        }
+        sw = pk["swap"]
+        if sw is not None:
+            n, bb = sw["blocks"], pk["wl"].geometry.block_bytes
+            rate = lambda ms: round(n * bb / (ms * 1e-3) / 1e9, 2)  # noqa: E731
+            ops_out["swap_through_pinned_host"] = {
+                "workload": f"Llama-2-13B swap through ops.swap: {n} of the {sw['of_blocks']} "
+                            f"scattered 12.5 MiB blocks out to pinned host and back into a "
+                            f"disjoint free set (scale {n / sw['of_blocks']:g})",
+                "blocks": n, "bytes_each_way": n * bb,
+                "swap_out_ms": round(sw["swap_out_ms"], 2), "swap_out_GB/s": rate(sw["swap_out_ms"]),
+                "swap_in_ms": round(sw["swap_in_ms"], 2), "swap_in_GB/s": rate(sw["swap_in_ms"]),
+                "legs": {"pack_ms": round(sw["pack_ms"], 3),
+                         "dma_d2h_ms": round(sw["dma_d2h_ms"], 2),
+                         "dma_d2h_GB/s": rate(sw["dma_d2h_ms"]),
+                         "dma_h2d_ms": round(sw["dma_h2d_ms"], 2),
+                         "dma_h2d_GB/s": rate(sw["dma_h2d_ms"]),
+                         "scatter_ms": round(sw["scatter_ms"], 3)},
+                "frac_pcie5_x16": round(rate(sw["swap_out_ms"]) / PCIE_PEAK_GBS, 4),
+                "pin_seconds": round(sw["pin_s"], 1)}
     if "defrag" in res:
         d = res["defrag"]
         dg = d["defrag_bytes"] / (d["defrag_ms"] * 1e-3) / 1e9
@@ -883,6 +1046,15 @@ def main(argv=None):
             "workload": "pack of 256 contiguous 1 MiB blocks (256 MiB read + 256 MiB write)",
             "us": round(c["ms"] * 1e3, 2), "bytes": c["bytes"], "GB/s": round(cg, 1),
             "frac_hbm": round(cg / HBM_PEAK_GBS, 4)}
+    if "floor" in res:
+        f = res["floor"]
+        fg = f["bytes"] / (f["ms"] * 1e-3) / 1e9
+        ops_out["copy_floor_at_append_bytes"] = {
+            "workload": "block-copy kernel, 14 contiguous 1 MiB blocks copied without id lists "
+                        "(29,360,128 B moved, the headline append's bytes less its slots), 32 "
+                        "rotated regions",
+            "us": round(f["ms"] * 1e3, 2), "bytes": f["bytes"], "GB/s": round(fg, 1),
+            "frac_hbm": round(fg / HBM_PEAK_GBS, 4)}
     line["ops"] = ops_out
     if cpu is not None:
         line["cpu_baseline"] = cpu

@@ -354,3 +354,68 @@ def test_oracle_swap_matches_per_byte_loop(data):
             d_pool[dst[i], byte] = s_pool[src[i], byte]
     ko.swap_blocks(src, dst, swap_in, dev, host)
     assert np.array_equal(dev, want_dev) and np.array_equal(host, want_host)
+
+
+# ---------------------------------------------------------------------------
+# the torch CPU restatement (the timed CPU baseline) against the numpy oracle
+# ---------------------------------------------------------------------------
+def _bits_tensor(bits, dtype):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(dtype)
+
+
+def test_torch_cpu_append_matches_oracle():
+    """Bit-exact against ko.append_layers, slot -1 skipped, blocks of other
+    sequences untouched (both start from the same poisoned pool)."""
+    from oracle import torch_cpu as tc
+    rng = np.random.default_rng(61)
+    N, L, H, D = 20, 3, 2, 64
+    pool = random_bits(rng, (N, L, 2, 16, H, D), "bf16")
+    key = random_bits(rng, (L, 9, H, D), "bf16")
+    val = random_bits(rng, (L, 9, H, D), "bf16")
+    slots = np.asarray([5, 17, 16, -1, 300, 31, 2, 319, 64], dtype=np.int64)
+    ref = pool.copy()
+    ko.append_layers(key, val, ref, slots)
+    got = _bits_tensor(pool.copy(), torch.bfloat16)
+    tc.append_layers(_bits_tensor(key, torch.bfloat16), _bits_tensor(val, torch.bfloat16), got,
+                     torch.from_numpy(slots))
+    assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), ref)
+
+
+def test_torch_cpu_attention_matches_oracle():
+    """float32 from 16-bit inputs within 1e-5 relative L2 of the float64
+    oracle (GQA 7, ragged lengths, a zero length, scattered tables)."""
+    from oracle import torch_cpu as tc
+    rng = np.random.default_rng(62)
+    lens = [1, 15, 16, 17, 0, 130]
+    need = [-(-x // 16) for x in lens]
+    N = 2 * sum(need) + 3
+    ids = rng.permutation(N)[:sum(need)]
+    tables, o = [], 0
+    for c in need:
+        tables.append([int(x) for x in ids[o:o + c]])
+        o += c
+    padded = ko.pad_block_tables(tables)
+    q = random_bits(rng, (len(lens), 14, 64), "bf16")
+    kc = random_bits(rng, (N, 16, 2, 64), "bf16")
+    vc = random_bits(rng, (N, 16, 2, 64), "bf16")
+    ref = ko.paged_decode_attention(ko.bits_to_float(q, "bf16"), ko.bits_to_float(kc, "bf16"),
+                                    ko.bits_to_float(vc, "bf16"), padded, lens, 0.125)
+    got = tc.paged_decode_attention(_bits_tensor(q, torch.bfloat16),
+                                    _bits_tensor(kc, torch.bfloat16),
+                                    _bits_tensor(vc, torch.bfloat16), torch.from_numpy(padded),
+                                    torch.tensor(lens), 0.125).double().numpy()
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-5
+    assert not got[4].any()
+
+
+def test_torch_cpu_swap_matches_oracle():
+    from oracle import torch_cpu as tc
+    rng = np.random.default_rng(63)
+    gpu = random_bits(rng, (12, 2, 16, 1, 64), "fp16")
+    host = np.zeros((6, 2, 16, 1, 64), dtype=np.uint16)
+    src, dst = [7, 2, 11, 2], [0, 5, 3, 1]
+    ref = host.copy()
+    ko.swap_blocks(src, dst, False, gpu.copy(), ref)
+    got = torch.from_numpy(host.copy().view(np.int16))
+    tc.swap_blocks(src, dst, torch.from_numpy(gpu.view(np.int16)), got)
+    assert np.array_equal(got.numpy().view(np.uint16), ref)
