@@ -27,6 +27,15 @@ SIGNATURES: Dict[str, tuple] = {
     "aegkv_init": (c_int, []),
     "aegkv_swap_blocks": (c_int, [_i64p, _i64p, c_int64, c_int, c_void_p, c_uint64, c_void_p,
                                   c_uint64, c_uint64, c_void_p, c_uint64, c_void_p]),
+    "aegkv_swap_blocks_bounced": (c_int, [_i64p, _i64p, c_int64, c_int, c_void_p, c_uint64,
+                                          c_void_p, c_uint64, c_uint64, c_void_p, c_uint64,
+                                          c_void_p, c_uint64, c_void_p]),
+    "aegkv_signals_create": (c_int, [c_int64, POINTER(c_void_p), c_void_p]),
+    "aegkv_signals_destroy": (c_int, [c_void_p]),
+    "aegkv_signals_open": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "aegkv_signals_close": (c_int, [c_void_p]),
+    "aegkv_signal_set": (c_int, [c_void_p, c_uint64, c_void_p]),
+    "aegkv_signal_wait": (c_int, [c_void_p, c_uint64, c_uint64, c_void_p, c_void_p]),
     "aegkv_copy_blocks": (c_int, [c_void_p, c_uint64, c_void_p, c_uint64, _i64p, _i64p, c_int64,
                                   c_uint64, c_void_p]),
     "aegkv_pack_blocks": (c_int, [c_void_p, c_uint64, _i64p, c_int64, c_void_p, c_uint64,

@@ -17,7 +17,9 @@
 // own load only (measured 4% faster on a contiguous 256 MiB copy than the
 // same loop with masked global loads and stores).
 #include <algorithm>
+#include <cstring>
 #include <numeric>
+#include <thread>
 
 #include "aegkv_internal.h"
 
@@ -309,6 +311,123 @@ int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
         if (e != hipSuccess) err = (int)e;
       });
       if (err) return err;
+      rc = with_uploaded_ids(ds, stream, &part, 1, [&](int64_t* ids) {
+        return launch_copy_blocks(ds, stg, dev, nullptr, ids, m, bb, stream);
+      });
+      if (rc) return rc;
+    }
+  }
+  return AEGKV_OK;
+}
+
+}  // extern "C"
+
+// ---- swap through a pageable host pool (the reference's /dev/shm file) ----
+namespace {
+
+// Host-side copies of one chunk, run by the HIP runtime in stream order
+// (hipLaunchHostFunc): between the pinned bounce buffer and the pageable
+// pool's blocks, spread over a few threads (a single thread copies ~10 GB/s).
+struct BounceChunk {
+  uint8_t* bounce;
+  uint8_t* pool;
+  uint64_t block_bytes;
+  bool to_pool;                 // bounce -> pool (swap-out) or pool -> bounce
+  std::vector<int64_t> ids;     // pool block of bounce slot k
+};
+
+void copy_bounce_chunk(void* user) {
+  BounceChunk* c = static_cast<BounceChunk*>(user);
+  const int64_t m = (int64_t)c->ids.size();
+  const uint64_t bytes = (uint64_t)m * c->block_bytes;
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const int nt = (int)std::min<uint64_t>({8, hw, std::max<uint64_t>(1, bytes >> 24)});
+  auto work = [c, m, nt](int t) {
+    // thread t copies an equal share of the chunk's bytes, block by block
+    const uint64_t bb = c->block_bytes;
+    const uint64_t total = (uint64_t)m * bb;
+    const uint64_t lo = total * t / nt, hi = total * (t + 1) / nt;
+    for (uint64_t off = lo; off < hi;) {
+      const uint64_t k = off / bb, in = off % bb;
+      const uint64_t len = std::min(bb - in, hi - off);
+      uint8_t* slot = c->bounce + off;
+      uint8_t* blk = c->pool + (uint64_t)c->ids[k] * bb + in;
+      if (c->to_pool) std::memcpy(blk, slot, len);
+      else std::memcpy(slot, blk, len);
+      off += len;
+    }
+  };
+  if (nt == 1) {
+    work(0);
+  } else {
+    std::vector<std::thread> th;
+    for (int t = 1; t < nt; ++t) th.emplace_back(work, t);
+    work(0);
+    for (auto& x : th) x.join();
+  }
+  delete c;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+                              int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
+                              void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
+                              void* staging, uint64_t staging_bytes, void* bounce,
+                              uint64_t bounce_bytes, aegkv_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  if (n < 0 || !dev_pool || !host_pool || !staging || !bounce || block_bytes == 0)
+    return AEGKV_ERR_INVALID_ARG;
+  if (n == 0) return AEGKV_OK;
+  if (!src_ids || !dst_ids) return AEGKV_ERR_INVALID_ARG;
+  const uint64_t n_src = is_swap_in ? n_host_blocks : n_dev_blocks;
+  const uint64_t n_dst = is_swap_in ? n_dev_blocks : n_host_blocks;
+  int rc;
+  if ((rc = check_ids_in_range(src_ids, n, n_src))) return rc;
+  if ((rc = check_ids_in_range(dst_ids, n, n_dst))) return rc;
+  if ((rc = check_unique(dst_ids, n))) return rc;
+  const uint64_t bb = block_bytes;
+  if ((bb & 15) || !aligned16(dev_pool) || !aligned16(staging)) return AEGKV_ERR_MISALIGNED;
+  const uint64_t cap64 = std::min(staging_bytes, bounce_bytes) / bb;
+  if (cap64 == 0) return AEGKV_ERR_WORKSPACE;
+  DeviceState* ds = nullptr;
+  if ((rc = current_device_state(&ds))) return rc;
+  uint8_t* dev = static_cast<uint8_t*>(dev_pool);
+  uint8_t* host = static_cast<uint8_t*>(host_pool);
+  uint8_t* stg = static_cast<uint8_t*>(staging);
+  uint8_t* bnc = static_cast<uint8_t*>(bounce);
+  const int64_t cap = (int64_t)std::min<uint64_t>(cap64, (uint64_t)n);
+  const int64_t* dev_key = is_swap_in ? dst_ids : src_ids;
+  const int64_t* host_key = is_swap_in ? src_ids : dst_ids;
+  for (int64_t c0 = 0; c0 < n; c0 += cap) {
+    const int64_t m = std::min(cap, n - c0);
+    BounceChunk* chunk = nullptr;
+    try {
+      chunk = new BounceChunk{bnc, host, bb, !is_swap_in,
+                              std::vector<int64_t>(host_key + c0, host_key + c0 + m)};
+    } catch (...) {
+      return AEGKV_ERR_RUNTIME;
+    }
+    IdPart part{dev_key + c0, m};
+    if (!is_swap_in) {
+      // pack the device blocks, DMA them to the bounce buffer, then the host
+      // copies them into the pool's blocks (the next chunk's DMA waits for it)
+      rc = with_uploaded_ids(ds, stream, &part, 1, [&](int64_t* ids) {
+        return launch_copy_blocks(ds, dev, stg, ids, nullptr, m, bb, stream);
+      });
+      if (rc) { delete chunk; return rc; }
+      hipError_t e = hipMemcpyAsync(bnc, stg, (uint64_t)m * bb, hipMemcpyDeviceToHost, stream);
+      if (e != hipSuccess) { delete chunk; return (int)e; }
+      e = hipLaunchHostFunc(stream, copy_bounce_chunk, chunk);
+      if (e != hipSuccess) { delete chunk; return (int)e; }
+    } else {
+      // the host gathers the pool's blocks into the bounce buffer, one DMA
+      // takes them to staging, and the scatter kernel places them
+      hipError_t e = hipLaunchHostFunc(stream, copy_bounce_chunk, chunk);
+      if (e != hipSuccess) { delete chunk; return (int)e; }
+      AEGKV_HIP_TRY(hipMemcpyAsync(stg, bnc, (uint64_t)m * bb, hipMemcpyHostToDevice, stream));
       rc = with_uploaded_ids(ds, stream, &part, 1, [&](int64_t* ids) {
         return launch_copy_blocks(ds, stg, dev, nullptr, ids, m, bb, stream);
       });

@@ -21,7 +21,7 @@ LIB_PATH = PKG / "libaegkv.so"
 
 SOURCES = [
     "runtime.hip", "blocks.hip", "append.hip", "attention.hip", "inputs.hip",
-    "prefill.hip", "block_manager.cpp",
+    "prefill.hip", "signals.hip", "block_manager.cpp",
 ]
 ARCH = "gfx950"
 

@@ -87,25 +87,35 @@ def _staging_for(device: torch.device, stream: int, need: int) -> torch.Tensor:
 
 def swap(source_block_ids: IdList, target_block_ids: IdList, is_swap_in: bool,
          kv_cache: torch.Tensor, kv_swap: torch.Tensor,
-         staging: Union[None, str, torch.Tensor] = "auto") -> None:
+         staging: Union[None, str, torch.Tensor] = "auto",
+         bounce: Optional[torch.Tensor] = None) -> None:
     """Copy block ``source_block_ids[i]`` to ``target_block_ids[i]`` between
-    the GPU cache and the pinned CPU swap space, CPU->GPU when ``is_swap_in``.
+    the GPU cache and the CPU swap space, CPU->GPU when ``is_swap_in``.
 
     ``kv_cache``: contiguous GPU tensor ``[N_gpu, *block_shape]``;
-    ``kv_swap``: contiguous pinned CPU tensor ``[N_cpu, *block_shape]`` or
-    flat (the reference pins its swap space, worker.py:130-147; a pageable
-    tensor would turn every DMA into a blocking copy, so it is rejected).
+    ``kv_swap``: contiguous CPU tensor ``[N_cpu, *block_shape]`` or flat,
+    pinned (the reference pins its swap space, worker.py:130-147), or
+    pageable together with ``bounce``: the reference's shared file mapping
+    where it cannot be page-locked (:func:`aegaeon_amd.swap_pool.init_cpu_cache`),
+    reached through the pinned uint8 ``bounce`` buffer
+    (aegkv_swap_blocks_bounced).  A pageable swap space without a bounce
+    buffer is rejected: every DMA would silently become a blocking copy.
     ``staging``: "auto" packs scattered GPU blocks through a per-stream device
     buffer so that each run of consecutive CPU ids is a single DMA; None issues
     one DMA per run of consecutive id pairs; a GPU uint8 tensor is used as the
-    staging buffer directly.
+    staging buffer directly.  The bounced path always stages.
     """
     _require_device(kv_cache, "kv_cache")
     if kv_swap.is_cuda or not kv_swap.is_contiguous():
         raise ValueError("kv_swap must be a contiguous CPU tensor")
-    if not kv_swap.is_pinned():
-        raise ValueError("kv_swap must be pinned host memory (torch pin_memory / hipHostMalloc): "
-                         "a pageable swap space makes every copy synchronous")
+    pinned = kv_swap.is_pinned()
+    if not pinned and bounce is None:
+        raise ValueError("kv_swap must be pinned host memory (torch pin_memory / hipHostMalloc), "
+                         "or pageable with a pinned bounce buffer: a pageable swap space makes "
+                         "every copy synchronous")
+    if bounce is not None and (bounce.is_cuda or not bounce.is_pinned()
+                               or not bounce.is_contiguous()):
+        raise ValueError("bounce must be a contiguous pinned CPU tensor")
     src, n = _ids(source_block_ids)
     dst, n2 = _ids(target_block_ids)
     if n != n2:
@@ -126,10 +136,18 @@ def swap(source_block_ids: IdList, target_block_ids: IdList, is_swap_in: bool,
             stg = staging
             if stg is not None and (not stg.is_cuda or stg.device != device):
                 raise ValueError(f"staging must be a GPU tensor on {device}")
+        if bounce is not None and not pinned and stg is None:
+            stg = _staging_for(device, stream, bb)
         stg_ptr, stg_bytes = (None, 0) if stg is None else (stg.data_ptr(), stg.numel() * stg.element_size())
-        rc = _lib.load().aegkv_swap_blocks(
-            _ptr(src), _ptr(dst), n, 1 if is_swap_in else 0, kv_cache.data_ptr(), n_dev,
-            kv_swap.data_ptr(), n_host, bb, stg_ptr, stg_bytes, stream)
+        if pinned:
+            rc = _lib.load().aegkv_swap_blocks(
+                _ptr(src), _ptr(dst), n, 1 if is_swap_in else 0, kv_cache.data_ptr(), n_dev,
+                kv_swap.data_ptr(), n_host, bb, stg_ptr, stg_bytes, stream)
+        else:
+            rc = _lib.load().aegkv_swap_blocks_bounced(
+                _ptr(src), _ptr(dst), n, 1 if is_swap_in else 0, kv_cache.data_ptr(), n_dev,
+                kv_swap.data_ptr(), n_host, bb, stg_ptr, stg_bytes, bounce.data_ptr(),
+                bounce.numel() * bounce.element_size(), stream)
     _lib.check(rc, "swap")
 
 

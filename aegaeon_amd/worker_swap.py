@@ -26,8 +26,17 @@ forward's K/V writes.  Here that order is explicit: a swap waits on the
 events passed as ``after`` (for example one recorded on the compute stream
 after the step's append), so the compute stream need not be synchronised.
 
-Cross-process handles of the events (the reference's ``reduce_cuda_event`` /
-``rebuild_cuda_event``, utils.py:306-331) are in :mod:`aegaeon_amd.swap_pool`.
+With ``interprocess=True`` every move also sets a word of the worker's
+:class:`aegaeon_amd.swap_pool.SignalArray` (one word per swap stream, the
+move's serial), :meth:`export` gives the handle another process waits on
+(the reference's ``reduce_cuda_event``, utils.py:306-315), and a source entry
+may be such a handle from another process: :meth:`swap_blocks` then makes its
+stream wait on that word, or, for a handle this process exported, on the
+request's own last event (``rebuild_cuda_event``, utils.py:318-331;
+worker.py:795-812).  A wait that times out sets :attr:`timed_out`
+(:meth:`check_timeouts`).  A pageable swap space (the shared file of
+:func:`aegaeon_amd.swap_pool.init_cpu_cache` where it cannot be page-locked)
+is reached through pinned bounce buffers the worker owns.
 """
 from __future__ import annotations
 
@@ -36,17 +45,22 @@ from typing import Dict, Iterable, List, Optional, Sequence, Union
 
 import torch
 
-from . import ops
+from . import ops, swap_pool
 
-EventLike = Union[torch.cuda.Event, Sequence[torch.cuda.Event], None]
+EventLike = Union[torch.cuda.Event, swap_pool.EventHandle, Sequence, None]
 
 
-def _events(x: EventLike) -> List[torch.cuda.Event]:
+def _is_handle(x) -> bool:
+    return isinstance(x, tuple) and len(x) == 5 and isinstance(x[2], (bytes, bytearray))
+
+
+def _events(x: EventLike) -> List:
+    """Flatten events and exported handles (kept as they are)."""
     if x is None:
         return []
-    if isinstance(x, torch.cuda.Event):
+    if isinstance(x, torch.cuda.Event) or _is_handle(x):
         return [x]
-    out: List[torch.cuda.Event] = []
+    out: List = []
     for e in x:
         out.extend(_events(e))
     return out
@@ -60,12 +74,20 @@ class KVSwapWorker:
     stream the forward runs on (default: the current stream)."""
 
     def __init__(self, kv_cache: torch.Tensor, kv_swap: torch.Tensor,
-                 compute_stream: Optional[torch.cuda.Stream] = None):
+                 compute_stream: Optional[torch.cuda.Stream] = None,
+                 interprocess: bool = False, bounce_bytes: int = 256 << 20):
         if not kv_cache.is_cuda:
             raise ValueError("kv_cache must be a GPU tensor")
         self.device = kv_cache.device
         self.kv_cache = kv_cache
         self.kv_swap = kv_swap
+        self.interprocess = interprocess
+        self.signals = swap_pool.SignalArray(2, self.device) if interprocess else None
+        self._serial = {True: 0, False: 0}       # per swap stream (word 1: swap-in)
+        self.timed_out = torch.zeros(1, dtype=torch.int32, device=self.device)
+        # one bounce buffer per direction: the two swap streams run concurrently
+        self.bounce = None if kv_swap.is_pinned() else {
+            d: swap_pool.bounce_buffer(bounce_bytes) for d in (True, False)}
         self.swap_in_stream = torch.cuda.Stream(device=self.device)
         self.swap_out_stream = torch.cuda.Stream(device=self.device)
         self.compute_stream = compute_stream or torch.cuda.current_stream(self.device)
@@ -85,12 +107,43 @@ class KVSwapWorker:
         new_event = torch.cuda.Event()
         self._wait_source_events(stream, new_event, request_ids, source_events)
         for e in _events(after):
-            stream.wait_event(e)
+            self._wait(stream, e, None)
         with torch.cuda.stream(stream):
             ops.swap(source_block_ids, target_block_ids, is_swap_in, self.kv_cache,
-                     self.kv_swap)
+                     self.kv_swap, bounce=None if self.bounce is None else self.bounce[is_swap_in])
         new_event.record(stream)
+        if self.signals is not None:
+            word = 1 if is_swap_in else 0
+            self._serial[is_swap_in] += 1
+            self.signals.signal(stream, word, self._serial[is_swap_in])
+            new_event.aegkv_signal = (word, self._serial[is_swap_in])
         return new_event
+
+    def export(self, event: torch.cuda.Event) -> swap_pool.EventHandle:
+        """The handle of a move of this worker that another process waits on
+        (``reduce_cuda_event``); needs ``interprocess=True``."""
+        if self.signals is None or not hasattr(event, "aegkv_signal"):
+            raise ValueError("only moves of an interprocess worker can be exported")
+        return swap_pool.reduce_event(self.signals, *event.aegkv_signal)
+
+    def check_timeouts(self) -> None:
+        """Raise if a wait on another process's move gave up (synchronises)."""
+        if int(self.timed_out.item()):
+            raise TimeoutError("a wait on another process's move timed out; the work behind it "
+                               "ran unordered")
+
+    def _wait(self, stream: torch.cuda.Stream, e, request_id: Optional[int]) -> None:
+        if _is_handle(e):
+            opened = swap_pool.rebuild_event(e)
+            if opened is None:  # exported by this process: the request's own event
+                evs = self.move_event_table.get(request_id) if request_id is not None else None
+                if evs:
+                    stream.wait_event(evs[-1])
+                return
+            arr, word, serial = opened
+            arr.wait(stream, word, serial, self.timed_out)
+            return
+        stream.wait_event(e)
 
     def _wait_source_events(self, stream: torch.cuda.Stream, new_event: torch.cuda.Event,
                             request_ids: Sequence[int],
@@ -107,7 +160,7 @@ class KVSwapWorker:
                 if not evs and self.move_event_table.get(rid):
                     evs = [self.move_event_table[rid][-1]]
                 for e in evs:
-                    stream.wait_event(e)
+                    self._wait(stream, e, rid)
             self.move_event_table[rid].append(new_event)
 
     # -- the compute side (worker.py:473-500) -------------------------------------

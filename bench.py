@@ -306,6 +306,9 @@ def bench_swap_host(args, wl, pool, staging, src, dst):
                                                staging=None))
     res["pack_ms"] = timed(lambda: ops.pack_blocks(pool, src[:n], out=staging[:n]))
     res["scatter_ms"] = timed(lambda: ops.scatter_blocks(staging[:n], dst[:n], pool))
+    # the reference's shared swap file, reached through a pinned bounce buffer
+    # (the file cannot be page-locked here): the same swap for a sample
+    res["file"] = bench_swap_file(pool, src, dst, bb, min(n, FILE_SWAP_BLOCKS), timed)
     # the round trip is bit-exact (checked here on a sample; the tests check all)
     k = torch.from_numpy(src[:min(n, 8)]).to(pool.device)
     j = torch.from_numpy(dst[:min(n, 8)]).to(pool.device)
@@ -318,6 +321,40 @@ def bench_swap_host(args, wl, pool, staging, src, dst):
     del host
     torch._C._host_emptyCache()
     return res
+
+
+FILE_SWAP_BLOCKS = 256          # 3.2 GiB of Llama-2-13B blocks in /dev/shm
+
+
+def bench_swap_file(pool, src, dst, bb, n, timed):
+    """ops.swap out to and back from a /dev/shm file of n blocks (the
+    reference's swap-space file, llm.py:297-318) through a 256 MiB pinned
+    bounce buffer, against the same call into pinned memory."""
+    import torch
+    import uuid
+    from aegaeon_amd import ops, swap_pool
+    path = f"/dev/shm/aegkv_bench_{os.getpid()}_{uuid.uuid4().hex[:6]}"
+    try:
+        kv_swap = swap_pool.init_cpu_cache(1, n * bb, path)
+        bounce = swap_pool.bounce_buffer(256 << 20)
+        ids = np.arange(n, dtype=np.int64)
+        out = {"blocks": n,
+               "swap_out_ms": timed(lambda: ops.swap(src[:n], ids, False, pool, kv_swap,
+                                                     bounce=bounce)),
+               "swap_in_ms": timed(lambda: ops.swap(ids, dst[:n], True, pool, kv_swap,
+                                                    bounce=bounce))}
+        k = torch.from_numpy(src[:4]).to(pool.device)
+        j = torch.from_numpy(dst[:4]).to(pool.device)
+        torch.cuda.synchronize()
+        if not torch.equal(pool[k], pool[j]):
+            raise RuntimeError("swap through the file is not bit-exact")
+        del kv_swap, bounce
+        return out
+    finally:
+        try:
+            os.unlink(path)
+        except FileNotFoundError:
+            pass
 
 
 # ------------------------------------------------------------- unified pool + defrag
@@ -986,6 +1023,18 @@ def main(argv=None):
                          "scatter_ms": round(sw["scatter_ms"], 3)},
                 "frac_pcie5_x16": round(rate(sw["swap_out_ms"]) / PCIE_PEAK_GBS, 4),
                 "pin_seconds": round(sw["pin_s"], 1)}
+            fl = sw.get("file")
+            if fl:
+                nf = fl["blocks"]
+                frate = lambda ms: round(nf * bb / (ms * 1e-3) / 1e9, 2)  # noqa: E731
+                ops_out["swap_through_shm_file"] = {
+                    "workload": f"the same swap for {nf} blocks into a /dev/shm file mapping "
+                                f"(the reference's shared swap space) through a 256 MiB pinned "
+                                f"bounce buffer",
+                    "swap_out_ms": round(fl["swap_out_ms"], 2),
+                    "swap_out_GB/s": frate(fl["swap_out_ms"]),
+                    "swap_in_ms": round(fl["swap_in_ms"], 2),
+                    "swap_in_GB/s": frate(fl["swap_in_ms"])}
     if "defrag" in res:
         d = res["defrag"]
         dg = d["defrag_bytes"] / (d["defrag_ms"] * 1e-3) / 1e9

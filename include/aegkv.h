@@ -84,6 +84,51 @@ int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
                       void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
                       void* staging, uint64_t staging_bytes, aegkv_stream_t stream);
 
+/* ---- a1 over a pageable swap space (the reference's shared file) --------
+ * The reference's swap space is one file in /dev/shm, mapped shared by every
+ * worker of the node and page-locked with cudaHostRegister
+ * (aegaeon/aegaeon/llm.py:297-318, worker.py:130-147).  Where that mapping
+ * cannot be page-locked, this is aegkv_swap_blocks with host_pool pageable:
+ * blocks cross a caller-owned pinned bounce buffer (bounce, bounce_bytes) and
+ * the device staging buffer (both required), chunk by chunk; the copies
+ * between the bounce buffer and host_pool run in stream order on the HIP
+ * runtime's host-function thread (hipLaunchHostFunc), so an event recorded on
+ * `stream` after the call completes only once host_pool holds the blocks
+ * (swap-out) or the device does (swap-in).  Same ids, checks and result as
+ * aegkv_swap_blocks.  host_pool, bounce and staging must stay valid until the
+ * stream has passed the call; chunks are min(staging, bounce) / block_bytes
+ * blocks (AEGKV_ERR_WORKSPACE when that is 0). */
+int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+                              int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
+                              void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
+                              void* staging, uint64_t staging_bytes, void* bounce,
+                              uint64_t bounce_bytes, aegkv_stream_t stream);
+
+/* ---- cross-process move signals ------------------------------------------
+ * Stand in for the interprocess CUDA events the reference's workers exchange
+ * (reduce_cuda_event / rebuild_cuda_event, aegaeon/aegaeon/utils.py:306-331;
+ * recorded after a swap at worker.py:740,765, waited on with
+ * cudaStreamWaitEvent at worker.py:772-815); on this runtime hipEventRecord
+ * refuses events created with hipEventInterprocess.  A signal array is
+ * n_words 64-bit timeline words of device memory (zeroed), created by one
+ * process with its 64-byte hipIpcMemHandle_t written to ipc_handle, opened by
+ * the others (aegkv_signals_open / _close; the creator frees it with
+ * aegkv_signals_destroy).  These four allocate, open or free device memory.
+ *   aegkv_signal_set: after the stream's earlier work, *word = value
+ *     (system-scope release).  One stream writes a word, with growing values.
+ *   aegkv_signal_wait: the stream's later work starts only once
+ *     *word >= value (a one-lane kernel polling with system-scope acquire
+ *     loads).  After timeout_us of wall-clock time it stops waiting and stores
+ *     1 to *timed_out (a DEVICE word, may be NULL), so the kernel always ends.
+ * word must be 8-byte aligned. */
+int aegkv_signals_create(int64_t n_words, void** words, void* ipc_handle);
+int aegkv_signals_destroy(void* words);
+int aegkv_signals_open(const void* ipc_handle, void** words);
+int aegkv_signals_close(void* words);
+int aegkv_signal_set(void* word, uint64_t value, aegkv_stream_t stream);
+int aegkv_signal_wait(const void* word, uint64_t value, uint64_t timeout_us, uint32_t* timed_out,
+                      aegkv_stream_t stream);
+
 /* ---- block gather / scatter / copy / defrag ----------------------------
  * Device-to-device block copies driven by HOST id lists (the lists the block
  * manager builds in move_requests, aegaeon/aegaeon/block_manager.py:822-832).

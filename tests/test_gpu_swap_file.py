@@ -1,0 +1,168 @@
+"""The shared swap-space file and cross-process move events on the GPU
+(aegaeon/aegaeon/llm.py:297-318, worker.py:130-147,716-815,
+utils.py:306-331).
+
+* The file mapping (the reference's layout: block b of a shape at byte
+  b * block_bytes, mapped shared as float16) reached through a pinned bounce
+  buffer: ops.swap out of and back into the GPU pool, with bounce buffers that
+  force several chunks, bit-exact against the oracle's swap; the file holds
+  what a second, independent mapping of it reads.
+* Two processes on the GPU sharing the file and exchanging move signals (the
+  stand-in for the reference's interprocess events, whose record this HIP
+  runtime refuses): the child swaps in what the parent swapped out, waiting
+  on the parent's exported move while the parent's swap-out is still held
+  behind a spin; then the parent swaps in what the child swapped out, waiting
+  on the child's.  Both sides check the bytes against seeded data, and
+  neither wait timed out.
+"""
+import json
+import os
+import queue
+import subprocess
+import sys
+import threading
+import uuid
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from aegaeon_amd import ops, swap_pool
+from aegaeon_amd.worker_swap import KVSwapWorker
+from oracle import kv_oracle as ko
+
+pytestmark = pytest.mark.gpu
+
+HERE = Path(__file__).resolve().parent
+SHAPE = (2, 2, 16, 4, 128)           # 64 KiB bf16 blocks
+BB = int(np.prod(SHAPE)) * 2
+N_SLABS, SLAB = 8, 4 << 20           # a 32 MiB file: 512 blocks
+
+
+@pytest.fixture
+def shm_path():
+    p = f"/dev/shm/aegkv_test_{os.getpid()}_{uuid.uuid4().hex[:8]}"
+    yield p
+    try:
+        os.unlink(p)
+    except FileNotFoundError:
+        pass
+
+
+def _seeded(seed, n):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-2 ** 15, 2 ** 15, (n, *SHAPE), dtype=torch.int16, generator=g)
+
+
+@pytest.mark.parametrize("bounce_blocks,staging_blocks", [(3, 5), (64, 64), (1, 1)])
+def test_swap_through_file_mapping(device, shm_path, bounce_blocks, staging_blocks):
+    """Swap-out into the shared file and swap-in back through bounce buffers
+    of 1-64 blocks (so 1 to 40 chunks), scattered ids on both sides."""
+    rng = np.random.default_rng(bounce_blocks)
+    kv_swap = swap_pool.init_cpu_cache(N_SLABS, SLAB, shm_path)
+    assert not kv_swap.is_pinned() and kv_swap.numel() * 2 == N_SLABS * SLAB
+    n_host = kv_swap.numel() * 2 // BB
+    N = 96
+    bits = _seeded(3, N)
+    cache = bits.view(torch.bfloat16).to(device)
+    src = rng.permutation(N)[:40]
+    host_ids = rng.permutation(n_host)[:40]
+    back = rng.permutation(np.setdiff1d(np.arange(N), src))[:40]
+    bounce = swap_pool.bounce_buffer(bounce_blocks * BB)
+    staging = torch.empty(staging_blocks * BB, dtype=torch.uint8, device=device)
+    ops.swap(src, host_ids, False, cache, kv_swap, staging=staging, bounce=bounce)
+    ops.swap(host_ids, back, True, cache, kv_swap, staging=staging, bounce=bounce)
+    torch.cuda.synchronize()
+    ref_gpu = bits.numpy().view(np.uint16).copy()
+    ref_host = np.zeros((n_host, *SHAPE), dtype=np.uint16)
+    ko.swap_blocks(src, host_ids, False, ref_gpu, ref_host)
+    ko.swap_blocks(host_ids, back, True, ref_gpu, ref_host)
+    assert np.array_equal(cache.view(torch.int16).cpu().numpy().view(np.uint16), ref_gpu)
+    # a second, independent mapping of the file reads the same bytes
+    again = swap_pool.init_cpu_cache(N_SLABS, SLAB, shm_path)
+    assert np.array_equal(again.view(torch.int16).numpy().view(np.uint16).reshape(ref_host.shape),
+                          ref_host)
+
+
+def test_pageable_swap_space_needs_a_bounce_buffer(device, shm_path):
+    kv_swap = swap_pool.init_cpu_cache(N_SLABS, SLAB, shm_path)
+    cache = torch.zeros((4, *SHAPE), dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError):
+        ops.swap([0], [0], False, cache, kv_swap)
+    with pytest.raises(ValueError):   # a bounce buffer that is not pinned
+        ops.swap([0], [0], False, cache, kv_swap, bounce=torch.empty(BB, dtype=torch.uint8))
+
+
+def test_two_processes_share_file_and_move_events(device, shm_path):
+    kv_swap = swap_pool.init_cpu_cache(N_SLABS, SLAB, shm_path)
+    cache = torch.zeros((64, *SHAPE), dtype=torch.bfloat16, device=device)
+    worker = KVSwapWorker(cache, kv_swap, interprocess=True, bounce_bytes=1 << 20)
+    err = open(shm_path + ".child.log", "w+")
+    child = subprocess.Popen([sys.executable, "-u", str(HERE / "swap_file_child.py"), shm_path,
+                              str(N_SLABS), str(SLAB)],
+                             stdin=subprocess.PIPE, stdout=subprocess.PIPE, stderr=err,
+                             text=True, cwd=str(HERE.parent))
+
+    lines = queue.Queue()
+    reader = threading.Thread(target=lambda: [lines.put(x) for x in child.stdout] + [lines.put("")],
+                              daemon=True)
+    reader.start()
+
+    def recv(timeout=90.0):
+        try:
+            line = lines.get(timeout=timeout)
+        except queue.Empty:
+            child.kill()
+            raise AssertionError("the child process did not answer in time")
+        if not line:
+            err.seek(0)
+            raise AssertionError(f"child ended early: {err.read()[-2000:]}")
+        return json.loads(line)
+
+    def send(obj):
+        child.stdin.write(json.dumps(obj) + "\n")
+        child.stdin.flush()
+
+    try:
+        assert recv() == {"ready": True}
+        hold = int(0.2 * 1.2e9)                 # ~200 ms of spin (~1.2 GHz shader clock)
+        dev_ids = list(range(0, 24))
+        file_ids = [int(x) for x in np.random.default_rng(4).permutation(256)[:24]]
+        cache[torch.tensor(dev_ids, device=device)] = _seeded(11, 24).to(device).view(
+            torch.bfloat16)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(worker.swap_out_stream):
+            torch.cuda._sleep(hold)             # the swap-out is still pending below
+        ev = worker.swap_blocks([1], dev_ids, file_ids, [None], False)
+        assert not ev.query()
+        d, pid, raw, word, serial = worker.export(ev)
+        out_file_ids = list(range(300, 316))
+        send({"handle": [d, pid, raw.hex(), word, serial], "file_ids": file_ids,
+              "dev_ids": list(range(40, 64)), "seed": 11, "out_file_ids": out_file_ids,
+              "out_seed": 12, "hold_cycles": hold})
+        reply = recv()
+        assert reply["ok"], reply["detail"]
+        # the child's swap-out is held behind its own spin: wait on its event
+        d2, pid2, raw2, w2, s2 = reply["handle"]
+        ev_in = worker.swap_blocks([8], out_file_ids, list(range(48, 64)),
+                                   [(int(d2), int(pid2), bytes.fromhex(raw2), int(w2), int(s2))],
+                                   True)
+        ev_in.synchronize()
+        worker.check_timeouts()
+        got = cache[48:64].view(torch.int16).cpu()
+        assert torch.equal(got, _seeded(12, 16))
+        # the parent's own mapping of the file holds the child's blocks too
+        host = kv_swap.view(torch.int16).view(-1, *SHAPE)
+        assert torch.equal(host[out_file_ids], _seeded(12, 16))
+        assert torch.equal(host[file_ids], _seeded(11, 24))
+        send({"done": True})
+        assert child.wait(timeout=60) == 0
+    finally:
+        if child.poll() is None:
+            child.kill()
+            child.wait()
+        torch.cuda.synchronize()
+        swap_pool.close_opened()
+        err.close()
+        os.unlink(shm_path + ".child.log")
