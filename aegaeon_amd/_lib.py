@@ -67,6 +67,22 @@ SIGNATURES: Dict[str, tuple] = {
                                                      c_int32, c_int32, c_int32, c_int32,
                                                      c_int32, c_float, c_int32, c_int32,
                                                      c_void_p]),
+    "aegkv_paged_decode_attention_append": (c_int, [c_void_p, c_int64, c_void_p, c_int64,
+                                                    c_void_p, c_int64, c_void_p, c_int64,
+                                                    c_void_p, c_void_p, c_int64, c_int64,
+                                                    c_void_p, c_int32, c_void_p, c_int32,
+                                                    c_int32, c_int32, c_int32, c_int32,
+                                                    c_int32, c_float, c_int32, c_int32,
+                                                    c_void_p, c_uint64, c_void_p]),
+    "aegkv_paged_decode_attention_append_planned": (c_int, [c_void_p, c_int64, c_void_p,
+                                                            c_int64, c_void_p, c_int64,
+                                                            c_void_p, c_int64, c_void_p,
+                                                            c_void_p, c_int64, c_int64,
+                                                            c_void_p, c_uint64, c_void_p,
+                                                            c_int32, c_int32, c_int32, c_int32,
+                                                            c_int32, c_int32, c_float, c_int32,
+                                                            c_int32, c_void_p, c_uint64,
+                                                            c_void_p]),
     "aegkv_paged_decode_plan_size": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
     "aegkv_paged_decode_plan": (c_int, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                         c_int32, c_void_p, c_uint64, c_void_p]),

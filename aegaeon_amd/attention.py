@@ -288,7 +288,9 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
                            scale: float, max_seq_len: int, out: Optional[torch.Tensor] = None,
                            n_workgroups: int = 0,
                            workspace: Optional[torch.Tensor] = None,
-                           plan: Optional[DecodePlan] = None) -> torch.Tensor:
+                           plan: Optional[DecodePlan] = None,
+                           key: Optional[torch.Tensor] = None,
+                           value: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Paged GQA decode attention: ``q [B, Hq, D]`` against per-layer cache
     views ``[N, 16, Hkv, D]``; returns ``out [B, Hq, D]`` in q's dtype.
     ``n_workgroups`` = 0 spreads the batch over one workgroup per CU; a
@@ -296,7 +298,14 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
     :func:`attention_workspace` (reusable on one stream); by default a cached
     one per (device, stream).  ``plan``: a :class:`DecodePlan` of this step's
     tables and lengths (then ``block_tables``/``seq_lens`` may be None, or
-    must be the tensors it was built from); the result is identical."""
+    must be the tensors it was built from); the result is identical.
+    ``key``/``value`` ``[B, Hkv, D]``: append them first, in the same call
+    (aegkv_paged_decode_attention_append): ``seq_lens[b]`` counts the new
+    token, which lands at position ``seq_lens[b] - 1`` of sequence b's table
+    (the slot the reference's slot mapping gives it); the output and the cache
+    equal those of :func:`reshape_and_cache_flash` followed by this call
+    without ``key``/``value``, bit for bit, at the cost of the attention's
+    launches alone."""
     if plan is not None:
         if plan.buffer.device != q.device:
             raise ValueError(f"the plan lives on {plan.buffer.device}, the call on {q.device}")
@@ -352,9 +361,33 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
                              f"bytes, the call needs {ws_bytes}")
     if plan is not None:
         plan.wait_for_build(torch.cuda.current_stream(dev))
+    if (key is None) != (value is None):
+        raise ValueError("key and value are appended together")
+    if key is not None:
+        for t, n in ((key, "key"), (value, "value")):
+            if t.dim() != 3 or t.shape != (B, Hkv, D) or t.dtype != q.dtype:
+                raise ValueError(f"{n} must be [B, Hkv, D] of q's dtype")
+            _check_rows(t, n)
+            _check_on(t, n, dev)
     ws_ptr = workspace.data_ptr() if (workspace is not None and ws_bytes > 0) else None
     with torch.cuda.device(q.device):
-        if plan is not None:
+        if key is not None:
+            kv = (key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0))
+            if plan is not None:
+                rc = _lib.load().aegkv_paged_decode_attention_append_planned(
+                    out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), *kv,
+                    key_cache.data_ptr(), value_cache.data_ptr(), key_cache.stride(0), N,
+                    plan.buffer.data_ptr(), plan.nbytes, sl.data_ptr(), B, max_seq_len, Hq, Hkv,
+                    D, bs, float(scale), _DTYPES[q.dtype], n_workgroups, ws_ptr,
+                    ws_bytes if ws_ptr else 0, _stream(q))
+            else:
+                rc = _lib.load().aegkv_paged_decode_attention_append(
+                    out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), *kv,
+                    key_cache.data_ptr(), value_cache.data_ptr(), key_cache.stride(0), N,
+                    bt.data_ptr(), bt.size(1), sl.data_ptr(), B, max_seq_len, Hq, Hkv, D, bs,
+                    float(scale), _DTYPES[q.dtype], n_workgroups, ws_ptr,
+                    ws_bytes if ws_ptr else 0, _stream(q))
+        elif plan is not None:
             rc = _lib.load().aegkv_paged_decode_attention_planned(
                 out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), key_cache.data_ptr(),
                 value_cache.data_ptr(), key_cache.stride(0), N, plan.buffer.data_ptr(),
@@ -371,23 +404,38 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
 
 
 def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                            block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+                            k: Optional[torch.Tensor] = None, v: Optional[torch.Tensor] = None,
+                            cache_seqlens: Optional[torch.Tensor] = None,
+                            block_table: Optional[torch.Tensor] = None,
                             softmax_scale: Optional[float] = None, causal: bool = True,
                             max_seqlen: Optional[int] = None,
                             out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """vllm-flash-attn's paged decode call for one query token per sequence:
     ``q [B, 1, Hq, D]`` -> ``[B, 1, Hq, D]``.  With a single query token the
     causal mask admits every cached token, so ``causal`` does not change the
-    result.  ``max_seqlen`` (host bound of cache_seqlens) defaults to
-    ``block_table.size(1) * block_size``."""
+    result.  ``max_seqlen`` (host bound of the attended lengths) defaults to
+    ``block_table.size(1) * block_size``.  With ``k``/``v`` ``[B, 1, Hkv, D]``
+    the new token is first written at position ``cache_seqlens[b]`` and the
+    attention covers ``cache_seqlens[b] + 1`` tokens (flash-attn's kvcache
+    semantics), in one fused call."""
     if q.dim() != 4 or q.size(1) != 1:
         raise NotImplementedError("decode only: q must be [B, 1, Hq, D]")
+    if cache_seqlens is None or block_table is None:
+        raise ValueError("cache_seqlens and block_table are required (paged cache)")
     B, _, Hq, D = q.shape
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
     bs = k_cache.size(1)
     ms = max_seqlen if max_seqlen is not None else block_table.size(1) * bs
-    o = paged_decode_attention(q.view(B, Hq, D), k_cache, v_cache, block_table, cache_seqlens,
-                               scale, ms, out=None if out is None else out.view(B, Hq, D))
+    key = value = None
+    seq_lens = cache_seqlens
+    if k is not None or v is not None:
+        if k is None or v is None or k.dim() != 4 or k.size(1) != 1 or v.shape != k.shape:
+            raise ValueError("k and v must both be [B, 1, Hkv, D]")
+        key, value = k[:, 0], v[:, 0]
+        seq_lens = cache_seqlens.to(torch.int32) + 1
+    o = paged_decode_attention(q.view(B, Hq, D), k_cache, v_cache, block_table, seq_lens,
+                               scale, ms, out=None if out is None else out.view(B, Hq, D),
+                               key=key, value=value)
     return o.view(B, 1, Hq, D)
 
 

@@ -166,16 +166,29 @@ struct AttnArgs {
   const int32_t* plan_wg;
   const int32_t* plan_first;
   const int32_t* plan_ids;
+  const int32_t* plan_tags;  // per item: new-row tag (see the plan layout)
+  const int32_t* plan_last;  // per sequence: its last block's id
+  // append fused into the call (knew == nullptr: none): the new token's K and
+  // V rows of sequence b, kv head h at knew/vnew + b * stride + h * D; the
+  // token is the last of seq_lens[b].  The main kernel reads it from there,
+  // the combine kernel's rows kHeadsPerGroup.. copy it into the cache.
+  const uint16_t* knew;
+  const uint16_t* vnew;
+  int64_t knew_bstride, vnew_bstride;  // elements
+  int32_t copy_rows;                   // combine grid rows that copy new rows
 };
 
 // Decode plan, in one device buffer: per main-kernel workgroup a record of 8
 // int32 (first kv-head group or -1 for an idle workgroup, last group, first
 // item and its sequence, end item in the last group, the batch's first
-// non-empty sequence), the merge descriptors, the block ids of the first 64
-// items of each workgroup's range, then the block ids of all items in item
-// order (item i = block i - bcum[b] of the sequence b holding it).
+// non-empty sequence), the merge descriptors, the block ids and new-row tags
+// of the first 64 items of each workgroup's range, each sequence's last block
+// id (-1 when empty), the block ids of all items in item order (item i =
+// block i - bcum[b] of the sequence b holding it), and their new-row tags
+// (b * 16 + the token offset of the last token in a sequence's last block,
+// -1 for other blocks), which an appending call uses.
 struct PlanLayout {
-  int64_t wg, desc, first, ids, total;
+  int64_t wg, desc, first, last, ids, tags, total;
 };
 inline PlanLayout plan_layout(int64_t batch, int64_t n_wg, int64_t nblk_max) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
@@ -183,8 +196,10 @@ inline PlanLayout plan_layout(int64_t batch, int64_t n_wg, int64_t nblk_max) {
   l.wg = 0;
   l.desc = up(n_wg * 32);
   l.first = l.desc + up(n_wg * 16);
-  l.ids = l.first + up(n_wg * 64 * 4);
-  l.total = l.ids + up(batch * nblk_max * 4);
+  l.last = l.first + up(n_wg * 128 * 4);
+  l.ids = l.last + up(batch * 4);
+  l.tags = l.ids + up(batch * nblk_max * 4);
+  l.total = l.tags + up(batch * nblk_max * 4);
   return l;
 }
 constexpr int kPlanRecord = 8;  // int32 per workgroup record
@@ -242,6 +257,25 @@ __device__ __forceinline__ void load_block(KVRegs<D>& r, const uint16_t* kh, con
     r.k[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kh + off + 32 * ks));
 #pragma unroll
   for (int c = 0; c < 4; ++c) load_words<KVRegs<D>::VW>(vh + off + c * row, r.v[c]);
+}
+
+// load_block for a sequence's last block when the call appends: the lanes
+// that hold the new token's row (token noff of the block) read it from the
+// append's input rows kn (K, this lane's dims) and vn (V) instead of the
+// cache, whose slot is written only after the attention.
+template <int D>
+__device__ __forceinline__ void load_block_new(KVRegs<D>& r, const uint16_t* kh,
+                                               const uint16_t* vh, int64_t off, int64_t row,
+                                               int noff, const uint16_t* kn, const uint16_t* vn) {
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15, g = lane >> 4;
+  const uint16_t* kp = j == noff ? kn : kh + off;
+#pragma unroll
+  for (int ks = 0; ks < KVRegs<D>::KS; ++ks)
+    r.k[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 32 * ks));
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    load_words<KVRegs<D>::VW>(4 * g + c == noff ? vn : vh + off + c * row, r.v[c]);
 }
 
 // Softmax update and P.V for one block whose first token is `tok0`; `len` is
@@ -434,11 +468,11 @@ __device__ __forceinline__ void get_record(const uint8_t* rec, f32x4* acc, float
 // holds the ids of items [i0, i0 + 64) when the caller loaded them (the
 // range's first pass), so no table lookup stands between the start and the
 // first K/V loads.
-template <int DT, int D, int NBUF, bool PLANNED>
+template <int DT, int D, int NBUF, bool PLANNED, bool FUSED>
 __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s_bcum,
                                              const int32_t* s_len, uint8_t* stage, int4* meta,
                                              int grp, int b0, int i0, int i1, bool have_first,
-                                             int id_first) {
+                                             int id_first, int tag_first) {
   constexpr int KS = D / 32;
   constexpr int DPL = D / 16;
   const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
@@ -462,28 +496,36 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
 
   // block id of item i (clamped into the range), one lane per item; bh is a
   // sequence at or before the item's (the item's own or the next one are
-  // checked before a search)
-  auto item_id = [&](int i, int bh) -> int {
+  // checked before a search).  An appending call also takes the item's
+  // new-row tag: b * 16 + the offset of sequence b's new token when the item
+  // is b's last block, else -1.
+  auto item_id = [&](int i, int bh, int& tag) -> int {
     i = min(i, i1 - 1);
     if constexpr (PLANNED) {
+      if constexpr (FUSED) tag = a.plan_tags[i];
       return a.plan_ids[i];
     } else {
       int b = bh;
       if (s_bcum[b + 1] <= i) b = s_bcum[b + 2] > i ? b + 1 : seq_at(s_bcum, a.batch, i);
+      if constexpr (FUSED)
+        tag = i == s_bcum[b + 1] - 1 ? b * kBlockSize + ((s_len[b] - 1) & (kBlockSize - 1)) : -1;
       return a.block_tables[(int64_t)b * a.max_blocks + (i - s_bcum[b])];
     }
   };
-  int id_cur = PLANNED && have_first ? id_first : item_id(i0 + lane, bc);  // [cbase, cbase + 64)
-  int id_nxt = item_id(i0 + 64 + lane, bc);  // items [cbase + 64, cbase + 128)
+  int tag_cur = tag_first, tag_nxt = -1;
+  int id_cur = PLANNED && have_first ? id_first : item_id(i0 + lane, bc, tag_cur);  // [cbase, +64)
+  int id_nxt = item_id(i0 + 64 + lane, bc, tag_nxt);  // items [cbase + 64, cbase + 128)
   int cbase = i0;
   // id of item i >= cbase (uniform): rotates the chunks when i leaves the
-  // current one; ids outside the pool become -1
-  auto id_at = [&](int i) -> int {
+  // current one; ids outside the pool become -1; `tag` gets the item's tag
+  auto id_at = [&](int i, int& tag) -> int {
     if (i - cbase >= 64) {
       id_cur = id_nxt;
+      tag_cur = tag_nxt;
       cbase += 64;
-      id_nxt = item_id(cbase + 64 + lane, bc);
+      id_nxt = item_id(cbase + 64 + lane, bc, tag_nxt);
     }
+    if constexpr (FUSED) tag = __builtin_amdgcn_readlane(tag_cur, i - cbase);
     const int id = __builtin_amdgcn_readlane(id_cur, i - cbase);
     return (id >= 0 && id < a.n_blocks) ? id : -1;
   };
@@ -560,22 +602,40 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
     }
   };
 
+  // An appending call swaps the new token's row into each sequence's last
+  // block by lane-wise address selects (no branch around the loads, so the
+  // compiler's wait counts stay exact).
+  const uint16_t* kn_lane = FUSED ? a.knew + (int64_t)h * D + 8 * g : nullptr;
+  const uint16_t* vn_lane = FUSED ? a.vnew + (int64_t)h * D + DPL * j : nullptr;
+  auto load_item = [&](KVRegs<D>& r, int id, int tag) {
+    const int64_t off = (int64_t)max(id, 0) * a.blk_stride;
+    if constexpr (FUSED) {
+      const int b = tag >> 4, noff = tag < 0 ? -1 : (tag & (kBlockSize - 1));
+      load_block_new<D>(r, kh, vh, off, row, noff, kn_lane + (int64_t)b * a.knew_bstride,
+                        vn_lane + (int64_t)b * a.vnew_bstride);
+    } else {
+      load_block<D>(r, kh, vh, off, row);
+    }
+  };
+
   const int n = i1 - i0;
   const int nfull = n - n % NBUF;
   KVRegs<D> buf[NBUF];
   int ids[NBUF];
   unrolled_steps<NBUF>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    ids[k] = id_at(min(i0 + k, i1 - 1));
-    load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
+    int tag = -1;
+    ids[k] = id_at(min(i0 + k, i1 - 1), tag);
+    load_item(buf[k], ids[k], tag);
     return false;
   });
   for (int it = 0; it < nfull; it += NBUF) {
     unrolled_steps<NBUF>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
       compute(buf[k], ids[k]);
-      ids[k] = id_at(min(i0 + it + k + NBUF, i1 - 1));
-      load_block<D>(buf[k], kh, vh, (int64_t)max(ids[k], 0) * a.blk_stride, row);
+      int tag = -1;
+      ids[k] = id_at(min(i0 + it + k + NBUF, i1 - 1), tag);
+      load_item(buf[k], ids[k], tag);
       return false;
     });
   }
@@ -669,7 +729,7 @@ __device__ __forceinline__ int64_t owner_of(int64_t P, int64_t total, int64_t n_
   return div_floor((P + 1) * n_act - 1, total);
 }
 
-template <int DT, int D, int NBUF, bool PLANNED>
+template <int DT, int D, int NBUF, bool PLANNED, bool FUSED>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, D >= 256 ? 1 : 2) void
 paged_decode_attention_kernel(AttnArgs a) {
   // cum[batch + 1] (positions), len[batch], bcum[batch + 1] (blocks)
@@ -686,11 +746,12 @@ paged_decode_attention_kernel(AttnArgs a) {
   // A planned workgroup's record and the block ids of its first 64 items,
   // loaded before the scan so that they arrive while it runs.
   int rec[kPlanRecord] = {};
-  int id_first = 0;
+  int id_first = 0, tag_first = -1;
   if constexpr (PLANNED) {
 #pragma unroll
     for (int k = 0; k < kPlanRecord; ++k) rec[k] = a.plan_wg[(int64_t)blockIdx.x * kPlanRecord + k];
-    id_first = a.plan_first[(int64_t)blockIdx.x * 64 + lane];
+    id_first = a.plan_first[(int64_t)blockIdx.x * 128 + lane];
+    if constexpr (FUSED) tag_first = a.plan_first[(int64_t)blockIdx.x * 128 + 64 + lane];
   }
   scan_batch(a.seq_lens, a.batch, a.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot);
   // Empty sequences have no positions: workgroup b % n_wg writes their zeros.
@@ -712,8 +773,9 @@ paged_decode_attention_kernel(AttnArgs a) {
       const int b0 = first_pass ? uni(rec[3]) : uni(rec[5]);
       const int i1 = grp == uni(rec[1]) ? uni(rec[4]) : items;
       if (i1 > i0)
-        attend_items<DT, D, NBUF, true>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0, i0, i1,
-                                        first_pass, id_first);
+        attend_items<DT, D, NBUF, true, FUSED>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0,
+                                               i0, i1, first_pass, id_first,
+                                               first_pass ? tag_first : -1);
     }
     return;
   }
@@ -765,8 +827,8 @@ paged_decode_attention_kernel(AttnArgs a) {
       first_pass = false;
     }
     if (i1 > i0)
-      attend_items<DT, D, NBUF, false>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0, i0, i1,
-                                       false, 0);
+      attend_items<DT, D, NBUF, false, FUSED>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0,
+                                              i0, i1, false, 0, -1);
     P = q_end;
     __syncthreads();  // s_find is rewritten by the next pass
   }
@@ -783,7 +845,9 @@ struct PlanArgs {
   int32_t* wg;
   int4* desc;
   int32_t* first;
+  int32_t* last;
   int32_t* ids;
+  int32_t* tags;
 };
 
 // Builds a decode plan (see PlanLayout) with the partition the attention
@@ -853,14 +917,27 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
     const int b = seq_at(s_bcum, p.batch, i);
     return p.block_tables[(int64_t)b * p.max_blocks + (i - s_bcum[b])];
   };
+  auto tag_of = [&](int i) -> int32_t {
+    const int b = seq_at(s_bcum, p.batch, i);
+    return i == s_bcum[b + 1] - 1 ? b * kBlockSize + ((s_len[b] - 1) & (kBlockSize - 1)) : -1;
+  };
   for (int64_t e = gtid; e < (int64_t)p.n_wg * 64; e += gsz) {
     const int w = (int)(e >> 6);
     if (w >= n_act) continue;
     const Range r = range_of(w);
     if (r.i1f <= r.i0) continue;  // the first pass holds no block
-    p.first[e] = id_of(min(r.i0 + (int)(e & 63), r.i1f - 1));
+    const int i = min(r.i0 + (int)(e & 63), r.i1f - 1);
+    p.first[(int64_t)w * 128 + (e & 63)] = id_of(i);
+    p.first[(int64_t)w * 128 + 64 + (e & 63)] = tag_of(i);
   }
-  for (int i = gtid; i < items; i += gsz) p.ids[i] = id_of(i);
+  for (int i = gtid; i < items; i += gsz) {
+    p.ids[i] = id_of(i);
+    p.tags[i] = tag_of(i);
+  }
+  for (int b = gtid; b < p.batch; b += gsz)
+    p.last[b] = s_len[b] > 0
+                    ? p.block_tables[(int64_t)b * p.max_blocks + (s_len[b] - 1) / kBlockSize]
+                    : -1;
 }
 
 // Merge the pieces of the cut sequence whose last block workgroup
@@ -876,6 +953,41 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
 // piece per load round keeps the kernel at 91 VGPRs and every workgroup
 // resident (Qwen2.5-7B batch: two pieces per round, 156 VGPRs, measured
 // 0.5 us per layer slower; four, 268 VGPRs, 8 us slower).
+// The cache write of an appending call, in the combine's extra grid rows
+// (blockIdx.y >= kHeadsPerGroup), which run beside the merges: the new
+// token's K and V rows of every sequence and kv head go to token
+// (len - 1) % 16 of the sequence's last block, 16 bytes per lane.  The main
+// kernel read those rows from the append's input, so nothing reads the slot
+// before this write.  Blocks outside the pool are skipped, as the attention
+// masks them.
+template <int D>
+__device__ __forceinline__ void copy_new_rows(const AttnArgs& a) {
+  constexpr int C = D / 8;  // 16-byte chunks of one kv head's row
+  const int64_t total = (int64_t)a.batch * a.n_kv_heads * 2 * C;
+  const int64_t stride = (int64_t)a.copy_rows * gridDim.x * blockDim.x;
+  const int64_t row = (int64_t)a.n_kv_heads * D;
+  for (int64_t c = ((int64_t)(blockIdx.y - kHeadsPerGroup) * gridDim.x + blockIdx.x) *
+                           blockDim.x + threadIdx.x;
+       c < total; c += stride) {
+    const int chunk = (int)(c % C);
+    const int64_t rest = c / C;
+    const int kv = (int)(rest & 1);
+    const int h = (int)((rest >> 1) % a.n_kv_heads);
+    const int b = (int)((rest >> 1) / a.n_kv_heads);
+    const int len = min(max(a.seq_lens[b], 0), a.max_seq_len);
+    if (len == 0) continue;
+    const int blk = a.plan_last ? a.plan_last[b]
+                                : a.block_tables[(int64_t)b * a.max_blocks + (len - 1) / kBlockSize];
+    if (blk < 0 || blk >= a.n_blocks) continue;
+    const uint16_t* src = (kv ? a.vnew + (int64_t)b * a.vnew_bstride
+                              : a.knew + (int64_t)b * a.knew_bstride) + (int64_t)h * D + 8 * chunk;
+    uint16_t* dst = const_cast<uint16_t*>(kv ? a.vc : a.kc) + (int64_t)blk * a.blk_stride +
+                    (int64_t)((len - 1) % kBlockSize) * row + (int64_t)h * D + 8 * chunk;
+    __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src)),
+                                reinterpret_cast<u32x4*>(dst));
+  }
+}
+
 template <int DT, int D, int KI>
 __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(AttnArgs a) {
   using E = Elem<DT>;
@@ -884,6 +996,10 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(
   __shared__ float s_m[kHeadsPerGroup - 1][KI][64];
   __shared__ float s_l[kHeadsPerGroup - 1][KI][64];
   __shared__ f32x4 s_o[kHeadsPerGroup - 1][KI][64];
+  if (blockIdx.y >= kHeadsPerGroup) {      // uniform: a row of the append's copy
+    copy_new_rows<D>(a);
+    return;
+  }
   const int4 d = a.desc[blockIdx.x];
   if (d.x < 0) return;  // uniform over the workgroup
   const int b = d.x, grp = d.y, npieces = d.w;
@@ -1005,20 +1121,28 @@ bool positions_fit(int64_t chunk, int64_t nblk_max, int64_t n_groups, int64_t n_
 
 template <int DT, int D, int KI>
 int launch_combine(const AttnArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI>), dim3(a.n_wg, kHeadsPerGroup),
-                     dim3(64 * kHeadsPerGroup), 0, stream, a);
+  hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI>),
+                     dim3(a.n_wg, kHeadsPerGroup + a.copy_rows), dim3(64 * kHeadsPerGroup), 0,
+                     stream, a);
   AEGKV_HIP_TRY(hipGetLastError());
   return AEGKV_OK;
 }
 
+template <int DT, int D, bool PLANNED, bool FUSED>
+void launch_main(const AttnArgs& a, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>(), PLANNED, FUSED>),
+                     dim3(a.n_wg), dim3(64 * kHeadsPerGroup), lds, stream, a);
+}
+
 template <int DT, int D>
 int launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
-  if (a.plan_wg)
-    hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>(), true>),
-                       dim3(a.n_wg), dim3(64 * kHeadsPerGroup), lds, stream, a);
-  else
-    hipLaunchKernelGGL((paged_decode_attention_kernel<DT, D, pipeline_depth<D>(), false>),
-                       dim3(a.n_wg), dim3(64 * kHeadsPerGroup), lds, stream, a);
+  if (a.plan_wg) {
+    if (a.knew) launch_main<DT, D, true, true>(a, lds, stream);
+    else launch_main<DT, D, true, false>(a, lds, stream);
+  } else {
+    if (a.knew) launch_main<DT, D, false, true>(a, lds, stream);
+    else launch_main<DT, D, false, false>(a, lds, stream);
+  }
   AEGKV_HIP_TRY(hipGetLastError());
   const int items = a.group * (D / 4);  // <= 16 * D / 4
   if (items <= 64) return launch_combine<DT, D, 1>(a, stream);
@@ -1035,13 +1159,22 @@ namespace aegkv {
 namespace {
 // Both entry points: `plan` (with plan_bytes) replaces the block tables when
 // given.
+// The new token's K/V rows of an appending call (none: key == nullptr).
+struct NewRows {
+  const void* key = nullptr;
+  int64_t key_bstride = 0;
+  const void* value = nullptr;
+  int64_t value_bstride = 0;
+};
+
 int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride,
                   const void* key_cache, const void* value_cache, int64_t cache_block_stride,
                   int64_t n_blocks, const int32_t* block_tables, int32_t max_blocks,
                   const void* plan, uint64_t plan_bytes, const int32_t* seq_lens, int32_t batch,
                   int32_t max_seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
                   int32_t block_size, float scale, int32_t dtype, int32_t n_workgroups,
-                  void* workspace, uint64_t workspace_bytes, aegkv_stream_t stream) {
+                  void* workspace, uint64_t workspace_bytes, aegkv_stream_t stream,
+                  const NewRows& nr = NewRows()) {
   if (batch < 0 || max_seq_len < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_blocks < 0 ||
       n_blocks < 0 || n_workgroups < 0)
     return AEGKV_ERR_INVALID_ARG;
@@ -1059,6 +1192,14 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
       ((cache_block_stride * 2) & 15))
     return AEGKV_ERR_MISALIGNED;
   if (n_q_heads > 65535 || n_workgroups > kMaxWorkgroups) return AEGKV_ERR_UNSUPPORTED;
+  if (nr.key) {
+    if (!nr.value || nr.key_bstride < (int64_t)n_kv_heads * head_dim ||
+        nr.value_bstride < (int64_t)n_kv_heads * head_dim)
+      return AEGKV_ERR_INVALID_ARG;
+    if (!aligned16(nr.key) || !aligned16(nr.value) || ((nr.key_bstride * 2) & 15) ||
+        ((nr.value_bstride * 2) & 15))
+      return AEGKV_ERR_MISALIGNED;
+  }
   const int64_t nblk_max = ((int64_t)max_seq_len + kBlockSize - 1) / kBlockSize;
   if (!plan && nblk_max > max_blocks) return AEGKV_ERR_INVALID_ARG;
   const int32_t chunk = std::min(batch, kMaxBatch);
@@ -1091,7 +1232,12 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
   a.q_bstride = q_batch_stride;
   a.out_bstride = out_batch_stride;
   a.desc = reinterpret_cast<int4*>(ws);
-  a.plan_wg = a.plan_first = a.plan_ids = nullptr;
+  a.plan_wg = a.plan_first = a.plan_ids = a.plan_last = a.plan_tags = nullptr;
+  a.knew = static_cast<const uint16_t*>(nr.key);
+  a.vnew = static_cast<const uint16_t*>(nr.value);
+  a.knew_bstride = nr.key_bstride;
+  a.vnew_bstride = nr.value_bstride;
+  a.copy_rows = 0;
   if (plan) {
     const PlanLayout pl = plan_layout(batch, n_wg, nblk_max);
     if (plan_bytes < (uint64_t)pl.total) return AEGKV_ERR_INVALID_ARG;
@@ -1100,7 +1246,9 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
     a.plan_wg = reinterpret_cast<const int32_t*>(pb + pl.wg);
     a.desc = reinterpret_cast<int4*>(const_cast<uint8_t*>(pb + pl.desc));
     a.plan_first = reinterpret_cast<const int32_t*>(pb + pl.first);
+    a.plan_last = reinterpret_cast<const int32_t*>(pb + pl.last);
     a.plan_ids = reinterpret_cast<const int32_t*>(pb + pl.ids);
+    a.plan_tags = reinterpret_cast<const int32_t*>(pb + pl.tags);
   }
   a.part_ml = reinterpret_cast<float2*>(ws + lay.desc_bytes);
   a.part_o = reinterpret_cast<float*>(ws + lay.desc_bytes + lay.ml_bytes);
@@ -1117,6 +1265,14 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
     a.out = static_cast<uint16_t*>(out) + (int64_t)c * out_batch_stride;
     a.block_tables = block_tables ? block_tables + (int64_t)c * max_blocks : nullptr;
     a.seq_lens = seq_lens + c;
+    if (nr.key) {
+      a.knew = static_cast<const uint16_t*>(nr.key) + (int64_t)c * nr.key_bstride;
+      a.vnew = static_cast<const uint16_t*>(nr.value) + (int64_t)c * nr.value_bstride;
+      // enough combine rows that each copy lane moves about one 16-byte chunk
+      const int64_t chunks = (int64_t)a.batch * n_kv_heads * 2 * (head_dim / 8);
+      const int64_t per_row = (int64_t)n_wg * 64 * kHeadsPerGroup;
+      a.copy_rows = (int32_t)std::min<int64_t>(64, std::max<int64_t>(1, (chunks + per_row - 1) / per_row));
+    }
     const size_t lds = lds_bytes(a, ds->max_lds);
     switch (head_dim) {
       case 64: rc = bf ? launch_attention<AEGKV_DTYPE_BF16, 64>(a, lds, st)
@@ -1232,6 +1388,47 @@ int aegkv_paged_decode_attention(void* out, int64_t out_batch_stride, const void
                        stream);
 }
 
+int aegkv_paged_decode_attention_append(
+    void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride, const void* key,
+    int64_t key_batch_stride, const void* value, int64_t value_batch_stride, void* key_cache,
+    void* value_cache, int64_t cache_block_stride, int64_t n_blocks, const int32_t* block_tables,
+    int32_t max_blocks, const int32_t* seq_lens, int32_t batch, int32_t max_seq_len,
+    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+    int32_t dtype, int32_t n_workgroups, void* workspace, uint64_t workspace_bytes,
+    aegkv_stream_t stream) {
+  if (batch > 0 && (!block_tables || !key || !value)) return AEGKV_ERR_INVALID_ARG;
+  NewRows nr;
+  nr.key = key;
+  nr.key_bstride = key_batch_stride;
+  nr.value = value;
+  nr.value_bstride = value_batch_stride;
+  return run_attention(out, out_batch_stride, q, q_batch_stride, key_cache, value_cache,
+                       cache_block_stride, n_blocks, block_tables, max_blocks, nullptr, 0,
+                       seq_lens, batch, max_seq_len, n_q_heads, n_kv_heads, head_dim,
+                       block_size, scale, dtype, n_workgroups, workspace, workspace_bytes,
+                       stream, nr);
+}
+
+int aegkv_paged_decode_attention_append_planned(
+    void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride, const void* key,
+    int64_t key_batch_stride, const void* value, int64_t value_batch_stride, void* key_cache,
+    void* value_cache, int64_t cache_block_stride, int64_t n_blocks, const void* plan,
+    uint64_t plan_bytes, const int32_t* seq_lens, int32_t batch, int32_t max_seq_len,
+    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+    int32_t dtype, int32_t n_workgroups, void* workspace, uint64_t workspace_bytes,
+    aegkv_stream_t stream) {
+  if (batch > 0 && (!plan || !key || !value)) return AEGKV_ERR_INVALID_ARG;
+  NewRows nr;
+  nr.key = key;
+  nr.key_bstride = key_batch_stride;
+  nr.value = value;
+  nr.value_bstride = value_batch_stride;
+  return run_attention(out, out_batch_stride, q, q_batch_stride, key_cache, value_cache,
+                       cache_block_stride, n_blocks, nullptr, 0, plan, plan_bytes, seq_lens,
+                       batch, max_seq_len, n_q_heads, n_kv_heads, head_dim, block_size, scale,
+                       dtype, n_workgroups, workspace, workspace_bytes, stream, nr);
+}
+
 int64_t aegkv_paged_decode_plan_size(int32_t batch, int32_t n_kv_heads, int32_t max_seq_len,
                                      int32_t n_workgroups) {
   if (batch < 0 || n_kv_heads <= 0 || max_seq_len < 0 || n_workgroups < 0)
@@ -1275,7 +1472,9 @@ int aegkv_paged_decode_plan(const int32_t* block_tables, int32_t max_blocks,
   p.wg = reinterpret_cast<int32_t*>(pb + pl.wg);
   p.desc = reinterpret_cast<int4*>(pb + pl.desc);
   p.first = reinterpret_cast<int32_t*>(pb + pl.first);
+  p.last = reinterpret_cast<int32_t*>(pb + pl.last);
   p.ids = reinterpret_cast<int32_t*>(pb + pl.ids);
+  p.tags = reinterpret_cast<int32_t*>(pb + pl.tags);
   const int64_t work = std::max<int64_t>((int64_t)n_wg * 64, (int64_t)batch * nblk_max);
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(1024, (work + 255) / 256));
   hipLaunchKernelGGL(decode_plan_kernel, dim3(grid), dim3(64 * kHeadsPerGroup),

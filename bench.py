@@ -206,6 +206,33 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
                                  max_len, out=outs[layer], n_workgroups=args.nwg,
                                  workspace=ws, plan=plan[0])
 
+    # The decode step as a layer runs it: the new token's K/V appended, then
+    # attention over seq_len tokens (the new one included).  Two launches per
+    # layer as vLLM does (reshape_and_cache_flash, then the attention), or
+    # the fused call (the append inside the attention's launches).
+    knew = torch.randn((g.n_layers, wb.batch, g.n_kv_heads, g.head_dim), generator=gen,
+                       device=dev).to(torch.bfloat16)
+    vnew = torch.randn(knew.shape, generator=gen, device=dev).to(torch.bfloat16)
+    slots = torch.from_numpy(wb.slot_mapping()).to(dev)
+
+    def two_launch_call(i):
+        layer = i % g.n_layers
+        if layer == 0:
+            plan[0] = A.DecodePlan(bt, sl, max_len, g.n_kv_heads, args.nwg)
+        A.reshape_and_cache_flash(knew[layer], vnew[layer], view[layer, 0], view[layer, 1], slots)
+        A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], None, None, scale,
+                                 max_len, out=outs[layer], n_workgroups=args.nwg,
+                                 workspace=ws, plan=plan[0])
+
+    def fused_call(i):
+        layer = i % g.n_layers
+        if layer == 0:
+            plan[0] = A.DecodePlan(bt, sl, max_len, g.n_kv_heads, args.nwg)
+        A.paged_decode_attention(q[layer], view[layer, 0], view[layer, 1], None, None, scale,
+                                 max_len, out=outs[layer], n_workgroups=args.nwg,
+                                 workspace=ws, plan=plan[0], key=knew[layer],
+                                 value=vnew[layer])
+
     for i in range(g.n_layers):
         layer_call(i)
     torch.cuda.synchronize()
@@ -215,15 +242,27 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
     torch.cuda.synchronize()
     if not torch.equal(outs, unplanned_out):
         raise RuntimeError("planned and unplanned attention disagree")
-    del unplanned_out
+    for i in range(g.n_layers):
+        two_launch_call(i)
+    torch.cuda.synchronize()
+    two_out = outs.clone()
+    for i in range(g.n_layers):
+        fused_call(i)
+    torch.cuda.synchronize()
+    if not torch.equal(outs, two_out):
+        raise RuntimeError("fused and two-launch append + attention disagree")
+    del unplanned_out, two_out
     steps = max(g.n_layers, (args.steps // g.n_layers) * g.n_layers)
     unplanned_ms, _ = timer.run(layer_call, steps)
     region_ms, _ = timer.run(planned_call, steps)
+    two_ms, _ = timer.run(two_launch_call, steps)
+    fused_ms, _ = timer.run(fused_call, steps)
     nbytes = wb.attention_bytes()
     del cache
     torch.cuda.empty_cache()
     return {"label": label, "wb": wb, "bytes_per_layer": nbytes, "us_per_layer": region_ms * 1e3,
-            "unplanned_us_per_layer": unplanned_ms * 1e3}
+            "unplanned_us_per_layer": unplanned_ms * 1e3, "two_launch_us": two_ms * 1e3,
+            "fused_us": fused_ms * 1e3}
 
 
 # ------------------------------------------------------------------------ pack / swap
@@ -983,6 +1022,12 @@ def main(argv=None):
             "bytes_per_layer": t["bytes_per_layer"], "GB/s": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "unplanned_us_per_layer": round(t["unplanned_us_per_layer"], 2)}
+        ops_out["decode_layer_append_then_attention"] = {
+            "workload": "the same batch, each layer's new token appended then attended over "
+                        "seq_len tokens, one decode plan per step",
+            "two_launches_us_per_layer": round(t["two_launch_us"], 2),
+            "fused_us_per_layer": round(t["fused_us"], 2),
+            "bit_identical": True}
         if "value" not in line:
             line.update({"value": round(t["us_per_layer"], 2), "unit": "us/layer",
                          "higher_is_better": False})

@@ -268,6 +268,39 @@ int aegkv_paged_decode_attention_noalloc(void* out, int64_t out_batch_stride, co
                                          int32_t block_size, float scale, int32_t dtype,
                                          int32_t n_workgroups, aegkv_stream_t stream);
 
+/* Append fused into the attention (EXT flash_attn_with_kvcache with its k=
+ * and v= arguments; in vLLM 0.5.1's backend the same step is
+ * reshape_and_cache_flash followed by flash_attn_with_kvcache, one launch each
+ * per layer, worker.py:517-523).  key/value: the new token's rows
+ * [batch][n_kv_heads][head_dim] (batch strides in elements, 16-byte aligned);
+ * seq_lens[b] counts that token, which lands at position seq_lens[b] - 1:
+ * token (len - 1) % 16 of block block_tables[b][(len - 1) / 16], the slot the
+ * reference's slot mapping gives it (worker.py:628-633).  The output is that
+ * of aegkv_kv_append into the cache followed by
+ * aegkv_paged_decode_attention, bit for bit, and the cache holds the appended
+ * rows afterwards; the attention reads the new rows from key/value, and the
+ * cache write runs beside the merge of split sequences, so the call costs the
+ * attention's two launches.  Other arguments, limits and the workspace are
+ * aegkv_paged_decode_attention's; the planned form takes a plan built from
+ * these seq_lens.  A last block outside [0, n_blocks) is neither read nor
+ * written. */
+int aegkv_paged_decode_attention_append(
+    void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride, const void* key,
+    int64_t key_batch_stride, const void* value, int64_t value_batch_stride, void* key_cache,
+    void* value_cache, int64_t cache_block_stride, int64_t n_blocks, const int32_t* block_tables,
+    int32_t max_blocks, const int32_t* seq_lens, int32_t batch, int32_t max_seq_len,
+    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+    int32_t dtype, int32_t n_workgroups, void* workspace, uint64_t workspace_bytes,
+    aegkv_stream_t stream);
+int aegkv_paged_decode_attention_append_planned(
+    void* out, int64_t out_batch_stride, const void* q, int64_t q_batch_stride, const void* key,
+    int64_t key_batch_stride, const void* value, int64_t value_batch_stride, void* key_cache,
+    void* value_cache, int64_t cache_block_stride, int64_t n_blocks, const void* plan,
+    uint64_t plan_bytes, const int32_t* seq_lens, int32_t batch, int32_t max_seq_len,
+    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+    int32_t dtype, int32_t n_workgroups, void* workspace, uint64_t workspace_bytes,
+    aegkv_stream_t stream);
+
 /* Decode plan: the work split of aegkv_paged_decode_attention for one batch
  * of block tables and lengths, built once per decode step and shared by every
  * layer's call (the layers of a step attend over the same tables, as the

@@ -166,9 +166,11 @@ def test_decode_plan_host_checks(lib):
     size = lib.aegkv_paged_decode_plan_size
     up = lambda x: -(-x // 256) * 256  # noqa: E731
     # (batch, Hkv, max_seq_len, n_workgroups): records of 8 int32, descriptors,
-    # 64 first ids per workgroup, then batch * ceil(max_seq_len / 16) ids
+    # 64 first ids and 64 first tags per workgroup, one last-block id per
+    # sequence, then batch * ceil(max_seq_len / 16) ids and as many tags
     assert size(0, 4, 4096, 8) == 0
-    assert size(3, 4, 100, 8) == up(8 * 32) + up(8 * 16) + up(8 * 256) + up(3 * 7 * 4)
+    assert size(3, 4, 100, 8) == (up(8 * 32) + up(8 * 16) + up(8 * 512) + up(3 * 4)
+                                  + 2 * up(3 * 7 * 4))
     assert size(2049, 4, 100, 8) == UNSUP  # one launch's batch at most
     assert size(3, 0, 100, 8) == INVALID
     assert size(3, 4, -1, 8) == INVALID
@@ -236,3 +238,25 @@ def test_prefill_attention_host_checks(lib):
     assert call(batch=0, q=None, out=None) == OK    # nothing to do
     assert call(ms=0) == OK
     assert call(q=None) == INVALID
+
+
+def test_fused_append_host_checks(lib):
+    """The appending attention rejects a missing or misaligned new row and a
+    batch stride shorter than one token's rows, before any launch."""
+    raw, p = _buf(1 << 20)
+    f = lib.aegkv_paged_decode_attention_append
+    Hq, Hkv, D = 8, 4, 128
+
+    def call(key=p, kstride=Hkv * D, value=p, vstride=Hkv * D):
+        # out, q, key, value, caches, tables, lengths: host addresses never read here
+        return f(p, Hq * D, p, Hq * D, key, kstride, value, vstride, p, p, 16 * Hkv * D, 8, p, 4,
+                 p, 2, 64, Hq, Hkv, D, 16, 0.1, 0, 8, p, 1 << 20, None)
+
+    assert call(key=None) == INVALID
+    assert call(value=None) == INVALID
+    assert call(kstride=Hkv * D - 8) == INVALID
+    assert call(key=p + 8) == MISALIGNED
+    assert call(vstride=Hkv * D + 4) == MISALIGNED
+    g = lib.aegkv_paged_decode_attention_append_planned
+    assert g(p, Hq * D, p, Hq * D, None, Hkv * D, p, Hkv * D, p, p, 16 * Hkv * D, 8, p, 1 << 20,
+             p, 2, 64, Hq, Hkv, D, 16, 0.1, 0, 8, p, 1 << 20, None) == INVALID

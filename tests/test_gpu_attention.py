@@ -512,3 +512,143 @@ def test_yi_decode_step_after_unified_pool_defrag(device):
         _check(to_bits(out), ref, "bf16")
     del pool, typed, view
     torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------------------
+# append fused into the attention (flash_attn_with_kvcache with k=, v=)
+# ---------------------------------------------------------------------------
+def _fused_case(device, lens, L, Hq, Hkv, D, dtype, seed):
+    """A 6-d storage [N, L, 2, 16, Hkv, D] with scattered tables for
+    sequences of `lens` tokens (the last one is the new token), the new rows
+    and the slots the reference's slot mapping gives them."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    need = [-(-int(x) // 16) for x in lens]
+    N = 2 * sum(need) + 5
+    ids = rng.permutation(N)[:sum(need)]
+    tables, o = [], 0
+    for c in need:
+        tables.append([int(x) for x in ids[o:o + c]])
+        o += c
+    storage = to_device_bits(random_bits(rng, (N, L, 2, 16, Hkv, D), dtype), dtype, device)
+    key = to_device_bits(random_bits(rng, (len(lens), Hkv, D), dtype), dtype, device)
+    val = to_device_bits(random_bits(rng, (len(lens), Hkv, D), dtype), dtype, device)
+    q = to_device_bits(random_bits(rng, (len(lens), Hq, D), dtype), dtype, device)
+    slots = ko.slot_mapping(tables, lens - 1, lens)
+    return (lens, tables, storage, key, val, q,
+            torch.from_numpy(ko.pad_block_tables(tables)).to(device),
+            torch.from_numpy(lens.astype(np.int32)).to(device),
+            torch.from_numpy(slots).to(device))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("Hq,Hkv,D", [(28, 4, 128), (16, 1, 64), (6, 2, 256), (40, 40, 128)])
+@pytest.mark.parametrize("nwg", [0, 1, 7, 300])
+@pytest.mark.parametrize("planned", [False, True])
+def test_fused_append_equals_append_then_attention(device, dtype, Hq, Hkv, D, nwg, planned):
+    """The fused call's output and cache equal reshape_and_cache_flash
+    followed by the attention, bit for bit (new tokens at block offsets 0, 15
+    and in between, a one-token sequence, sequences split across
+    workgroups), and the output is within the float64 oracle's tolerance."""
+    lens = [1, 16, 17, 32, 33, 200, 517, 1100, 15, 64 * 16 + 1]
+    L, layer = 3, 1
+    lens, tables, storage, key, val, q, bt, sl, slots = _fused_case(device, lens, L, Hq, Hkv, D,
+                                                                    dtype, nwg + D + Hq)
+    ml = int(lens.max())
+    scale = 1.0 / math.sqrt(D)
+    two = storage.clone()
+    view2 = two.permute(1, 2, 0, 3, 4, 5)
+    A.reshape_and_cache_flash(key, val, view2[layer, 0], view2[layer, 1], slots)
+    plan = A.DecodePlan(bt, sl, ml, Hkv, nwg) if planned else None
+    ref = A.paged_decode_attention(q, view2[layer, 0], view2[layer, 1], bt, sl, scale, ml,
+                                   n_workgroups=nwg, plan=plan)
+    view = storage.permute(1, 2, 0, 3, 4, 5)
+    got = A.paged_decode_attention(q, view[layer, 0], view[layer, 1], bt, sl, scale, ml,
+                                   n_workgroups=nwg, plan=plan, key=key, value=val)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
+    kb = to_bits(two[:, layer, 0])
+    vb = to_bits(two[:, layer, 1])
+    oracle = ko.paged_decode_attention(ko.bits_to_float(to_bits(q), dtype),
+                                       ko.bits_to_float(kb, dtype), ko.bits_to_float(vb, dtype),
+                                       ko.pad_block_tables(tables), lens, scale)
+    _check(to_bits(got), oracle, dtype)
+
+
+def test_fused_append_batch_above_one_launch(device):
+    """2500 sequences (two launches of the unplanned kernel, several rows of
+    cache copies in the merge kernel): output and cache equal the two-launch
+    pattern's."""
+    rng = np.random.default_rng(51)
+    lens = rng.integers(1, 90, 2500)
+    lens, tables, storage, key, val, q, bt, sl, slots = _fused_case(device, lens, 1, 16, 8, 64,
+                                                                    "bf16", 52)
+    ml = int(lens.max())
+    two = storage.clone()
+    view2 = two.permute(1, 2, 0, 3, 4, 5)
+    A.reshape_and_cache_flash(key, val, view2[0, 0], view2[0, 1], slots)
+    ref = A.paged_decode_attention(q, view2[0, 0], view2[0, 1], bt, sl, 0.125, ml)
+    view = storage.permute(1, 2, 0, 3, 4, 5)
+    got = A.paged_decode_attention(q, view[0, 0], view[0, 1], bt, sl, 0.125, ml, key=key,
+                                   value=val)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
+
+
+def test_fused_append_qwen_full_batch(device):
+    """The Qwen2.5-7B decode batch (128 sequences up to 8192 tokens), planned,
+    in the 28-layer storage: the fused call equals the two-launch pattern for
+    every layer of a step that shares one plan."""
+    wb = qwen_attention_batch(0)
+    g = wb.geometry
+    gen = torch.Generator(device=device).manual_seed(53)
+    N = wb.n_pool_blocks
+    storage = torch.empty((N, 4, 2, 16, g.n_kv_heads, g.head_dim), dtype=torch.bfloat16,
+                          device=device)
+    storage.normal_(generator=gen)
+    two = storage.clone()
+    bt = torch.from_numpy(wb.padded_tables()).to(device)
+    sl = torch.from_numpy(wb.seq_lens.astype(np.int32)).to(device)
+    slots = torch.from_numpy(wb.slot_mapping()).to(device)
+    ml = int(wb.seq_lens.max())
+    plan = A.DecodePlan(bt, sl, ml, g.n_kv_heads)
+    view, view2 = storage.permute(1, 2, 0, 3, 4, 5), two.permute(1, 2, 0, 3, 4, 5)
+    for layer in range(4):
+        q = torch.randn((wb.batch, 28, 128), generator=gen, device=device).to(torch.bfloat16)
+        k = torch.randn((wb.batch, 4, 128), generator=gen, device=device).to(torch.bfloat16)
+        v = torch.randn((wb.batch, 4, 128), generator=gen, device=device).to(torch.bfloat16)
+        A.reshape_and_cache_flash(k, v, view2[layer, 0], view2[layer, 1], slots)
+        ref = A.paged_decode_attention(q, view2[layer, 0], view2[layer, 1], None, None,
+                                       1 / math.sqrt(128), ml, plan=plan)
+        got = A.paged_decode_attention(q, view[layer, 0], view[layer, 1], None, None,
+                                       1 / math.sqrt(128), ml, plan=plan, key=k, value=v)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), layer
+    assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
+
+
+def test_flash_attn_with_kvcache_appends(device):
+    """flash-attn's kvcache semantics: k/v land at position cache_seqlens[b]
+    and the attention covers cache_seqlens[b] + 1 tokens."""
+    rng = np.random.default_rng(54)
+    ctx = np.asarray([0, 15, 16, 70], dtype=np.int64)
+    lens, tables, storage, key, val, q, bt, sl, slots = _fused_case(device, ctx + 1, 1, 8, 2, 64,
+                                                                    "bf16", 55)
+    view = storage.permute(1, 2, 0, 3, 4, 5)
+    before = storage.clone()
+    out = A.flash_attn_with_kvcache(q.view(4, 1, 8, 64), view[0, 0], view[0, 1],
+                                    k=key.view(4, 1, 2, 64), v=val.view(4, 1, 2, 64),
+                                    cache_seqlens=torch.from_numpy(ctx.astype(np.int32)).to(device),
+                                    block_table=bt)
+    torch.cuda.synchronize()
+    kb = to_bits(before[:, 0, 0])
+    vb = to_bits(before[:, 0, 1])
+    ko.reshape_and_cache_flash(to_bits(key), to_bits(val), kb, vb, slots.cpu().numpy())
+    assert np.array_equal(to_bits(storage[:, 0, 0]), kb)
+    assert np.array_equal(to_bits(storage[:, 0, 1]), vb)
+    ref = ko.paged_decode_attention(ko.bits_to_float(to_bits(q), "bf16"),
+                                    ko.bits_to_float(kb, "bf16"), ko.bits_to_float(vb, "bf16"),
+                                    ko.pad_block_tables(tables), ctx + 1, 1 / math.sqrt(64))
+    _check(to_bits(out).reshape(4, 8, 64), ref, "bf16")
