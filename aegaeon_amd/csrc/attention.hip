@@ -226,16 +226,20 @@ inline WorkspaceLayout workspace_layout(int64_t batch, int64_t hpg, int64_t head
 
 // K/V are streamed once per decode step: non-temporal loads keep them from
 // displacing reusable lines in the caches (measured ~9% more read bandwidth
-// than ordinary loads on scattered 16-32 KiB regions).
+// than ordinary loads on scattered 16-32 KiB regions).  A block is read
+// through a raw buffer range over its K (or V) rows, so a load that must
+// issue but has nothing to read (a pipeline refill past the end of a range,
+// an unreadable block id) gets an empty range: it returns zeros and moves no
+// bytes, and the loop still issues every load unconditionally.
 template <int NW>
-__device__ __forceinline__ void load_words(const uint16_t* p, uint32_t* w) {
+__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t* w) {
   if constexpr (NW == 2) {
-    u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNt);
     w[0] = v.x; w[1] = v.y;
   } else {
 #pragma unroll
     for (int i = 0; i < NW / 4; ++i) {
-      u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 8 * i));
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, kNt);
       w[4 * i + 0] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
     }
   }
@@ -250,33 +254,54 @@ struct KVRegs {
   uint32_t v[4][VW];
 };
 
+// One block: kr / vr are the block's K and V rows (16 x n_kv_heads * D
+// elements each, or empty), koff / voff this lane's byte offsets in them
+// (K: token j, dims 8g + 32 ks; V: tokens 4g + c, dims D/16 * j), row_b the
+// bytes of one token row.
 template <int D>
-__device__ __forceinline__ void load_block(KVRegs<D>& r, const uint16_t* kh, const uint16_t* vh,
-                                           int64_t off, int64_t row) {
+__device__ __forceinline__ void load_block(KVRegs<D>& r, __amdgpu_buffer_rsrc_t kr,
+                                           __amdgpu_buffer_rsrc_t vr, uint32_t koff,
+                                           uint32_t voff, uint32_t row_b) {
 #pragma unroll
   for (int ks = 0; ks < KVRegs<D>::KS; ++ks)
-    r.k[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kh + off + 32 * ks));
+    r.k[ks] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff + 64 * ks, 0, kNt);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) load_words<KVRegs<D>::VW>(vh + off + c * row, r.v[c]);
+  for (int c = 0; c < 4; ++c) load_words<KVRegs<D>::VW>(vr, voff + c * row_b, r.v[c]);
 }
+
+// An offset past the end of every range (a block's rows are < 2^31 bytes).
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 // load_block for a sequence's last block when the call appends: the lanes
 // that hold the new token's row (token noff of the block) read it from the
-// append's input rows kn (K, this lane's dims) and vn (V) instead of the
-// cache, whose slot is written only after the attention.
+// append's input row (knr / vnr, this lane's dims at knoff / vnoff) instead of
+// the cache, whose slot is written only after the attention.  Both loads of a
+// word issue; the lane's offset is out of range in the one it does not use,
+// which then returns zero and reads nothing.
 template <int D>
-__device__ __forceinline__ void load_block_new(KVRegs<D>& r, const uint16_t* kh,
-                                               const uint16_t* vh, int64_t off, int64_t row,
-                                               int noff, const uint16_t* kn, const uint16_t* vn) {
+__device__ __forceinline__ void load_block_new(KVRegs<D>& r, __amdgpu_buffer_rsrc_t kr,
+                                               __amdgpu_buffer_rsrc_t vr, uint32_t koff,
+                                               uint32_t voff, uint32_t row_b, int noff,
+                                               __amdgpu_buffer_rsrc_t knr,
+                                               __amdgpu_buffer_rsrc_t vnr, uint32_t knoff,
+                                               uint32_t vnoff) {
   const int lane = threadIdx.x & 63;
   const int j = lane & 15, g = lane >> 4;
-  const uint16_t* kp = j == noff ? kn : kh + off;
+  const bool kn = j == noff;
+  const uint32_t kc_at = kn ? kOutOfRange : koff, kn_at = kn ? knoff : kOutOfRange;
 #pragma unroll
   for (int ks = 0; ks < KVRegs<D>::KS; ++ks)
-    r.k[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 32 * ks));
+    r.k[ks] = __builtin_amdgcn_raw_buffer_load_b128(kr, kc_at + 64 * ks, 0, kNt) |
+              __builtin_amdgcn_raw_buffer_load_b128(knr, kn_at + 64 * ks, 0, kNt);
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    load_words<KVRegs<D>::VW>(4 * g + c == noff ? vn : vh + off + c * row, r.v[c]);
+  for (int c = 0; c < 4; ++c) {
+    const bool vn = 4 * g + c == noff;
+    uint32_t wc[KVRegs<D>::VW], wn[KVRegs<D>::VW];
+    load_words<KVRegs<D>::VW>(vr, vn ? kOutOfRange : voff + c * row_b, wc);
+    load_words<KVRegs<D>::VW>(vnr, vn ? vnoff : kOutOfRange, wn);
+#pragma unroll
+    for (int w = 0; w < KVRegs<D>::VW; ++w) r.v[c][w] = wc[w] | wn[w];
+  }
 }
 
 // Softmax update and P.V for one block whose first token is `tok0`; `len` is
@@ -460,10 +485,12 @@ __device__ __forceinline__ void get_record(const uint8_t* rec, f32x4* acc, float
 // sequence and the start of the next.  A sequence piece that ends costs its
 // output stores and the switch to the next sequence, whose query was loaded
 // when the previous switch happened.  Inside the loop every K/V load is
-// issued unconditionally (a refill past the range re-reads its last block,
-// an L2 hit that is never computed).  Block ids come 64 items at a time, one
-// per lane, with the next 64 loaded a chunk ahead; an unreadable id loads
-// block 0 and is masked (the host guarantees n_blocks >= 1).
+// issued unconditionally: a refill past the range, and an unreadable block
+// id, load through an empty buffer range, which reads no memory (re-reading
+// the range's last block instead cost 4% more HBM traffic on the
+// Qwen2.5-7B batch and 12% on the Yi-1.5-9B one, as the non-temporal lines
+// were gone from L2).  Block ids come 64 items at a time, one per lane, with
+// the next 64 loaded a chunk ahead; an unreadable block is masked.
 //
 // With a plan (PLANNED) the ids come from its item-order list, and `id_first`
 // holds the ids of items [i0, i0 + 64) when the caller loaded them (the
@@ -484,8 +511,10 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   const int hq = h * a.group + j;
   const int hl0 = wave * a.group;
   const int64_t row = (int64_t)a.n_kv_heads * D;
-  const uint16_t* kh = a.kc + (int64_t)h * D + (int64_t)j * row + 8 * g;
-  const uint16_t* vh = a.vc + (int64_t)h * D + (int64_t)(4 * g) * row + DPL * j;
+  const uint32_t row_b = (uint32_t)(row * 2);
+  const uint32_t blk_b = kBlockSize * row_b;  // a block's K (or V) rows
+  const uint32_t koff = (uint32_t)(((int64_t)j * row + (int64_t)h * D + 8 * g) * 2);
+  const uint32_t voff = (uint32_t)(((int64_t)(4 * g) * row + (int64_t)h * D + DPL * j) * 2);
 
   // the sequence being computed: bc, whose block 0 is item `first`, with
   // items up to cend in range
@@ -606,16 +635,24 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   // An appending call swaps the new token's row into each sequence's last
   // block by lane-wise address selects (no branch around the loads, so the
   // compiler's wait counts stay exact).
-  const uint16_t* kn_lane = FUSED ? a.knew + (int64_t)h * D + 8 * g : nullptr;
-  const uint16_t* vn_lane = FUSED ? a.vnew + (int64_t)h * D + DPL * j : nullptr;
-  auto load_item = [&](KVRegs<D>& r, int id, int tag) {
+  // `valid`: the item is in the range (a refill past its end reads nothing)
+  auto load_item = [&](KVRegs<D>& r, int id, int tag, bool valid) {
+    const bool ok = valid && id >= 0;
     const int64_t off = (int64_t)max(id, 0) * a.blk_stride;
+    const auto kr = byte_range(reinterpret_cast<const uint8_t*>(a.kc + off), ok ? blk_b : 0u);
+    const auto vr = byte_range(reinterpret_cast<const uint8_t*>(a.vc + off), ok ? blk_b : 0u);
     if constexpr (FUSED) {
-      const int b = tag >> 4, noff = tag < 0 ? -1 : (tag & (kBlockSize - 1));
-      load_block_new<D>(r, kh, vh, off, row, noff, kn_lane + (int64_t)b * a.knew_bstride,
-                        vn_lane + (int64_t)b * a.vnew_bstride);
+      const int b = max(tag, 0) >> 4, noff = tag < 0 ? -1 : (tag & (kBlockSize - 1));
+      const bool nw = valid && tag >= 0;
+      const auto knr = byte_range(
+          reinterpret_cast<const uint8_t*>(a.knew + (int64_t)b * a.knew_bstride), nw ? row_b : 0u);
+      const auto vnr = byte_range(
+          reinterpret_cast<const uint8_t*>(a.vnew + (int64_t)b * a.vnew_bstride), nw ? row_b : 0u);
+      load_block_new<D>(r, kr, vr, koff, voff, row_b, noff, knr, vnr,
+                        (uint32_t)(((int64_t)h * D + 8 * g) * 2),
+                        (uint32_t)(((int64_t)h * D + DPL * j) * 2));
     } else {
-      load_block<D>(r, kh, vh, off, row);
+      load_block<D>(r, kr, vr, koff, voff, row_b);
     }
   };
 
@@ -627,7 +664,7 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
     constexpr int k = decltype(kc)::value;
     int tag = -1;
     ids[k] = id_at(min(i0 + k, i1 - 1), tag);
-    load_item(buf[k], ids[k], tag);
+    load_item(buf[k], ids[k], tag, i0 + k < i1);
     return false;
   });
   for (int it = 0; it < nfull; it += NBUF) {
@@ -636,7 +673,7 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
       compute(buf[k], ids[k]);
       int tag = -1;
       ids[k] = id_at(min(i0 + it + k + NBUF, i1 - 1), tag);
-      load_item(buf[k], ids[k], tag);
+      load_item(buf[k], ids[k], tag, i0 + it + k + NBUF < i1);
       return false;
     });
   }
@@ -945,15 +982,17 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
 // blockIdx.x of the main kernel held (none: nothing to do), for kv head
 // grp * 4 + blockIdx.y:
 //   out = sum_s w_s o_s / sum_s w_s l_s,  w_s = 2^(m_s - max m).
-// The kv head's G query heads x D/4 float4 columns are "items", spread densely
-// over the 64 lanes of a wave (KI = ceil(G * D/4 / 64) per lane, a template
-// parameter so that registers follow the group size); wave w merges pieces
-// w, w + 4, ... online, one at a time, and the four waves' states merge in LDS.
+// The kv head's G query heads x D/4 float4 columns are "items", one per
+// thread (KI per thread past 256 items); a thread loads the (m, l) and o of
+// up to PB pieces of its item at once and merges them in registers, so a
+// sequence of up to PB pieces costs one round trip and no LDS.  (Per-wave
+// pieces merged through LDS took one round trip per four pieces: per
+// workgroup timestamps put the combine's tail at 3.4 us of piece loads for a
+// nine-piece sequence against 1.7 us for two; this version measured 2.4 us
+// per layer faster on the Qwen2.5-7B batch and 1.9 us on the Yi-1.5-9B one.)
 // Most of the grid's workgroups hold no task and exit after the descriptor
-// load, so what bounds the kernel is how many of them a CU holds at once: one
-// piece per load round keeps the kernel at 91 VGPRs and every workgroup
-// resident (Qwen2.5-7B batch: two pieces per round, 156 VGPRs, measured
-// 0.5 us per layer slower; four, 268 VGPRs, 8 us slower).
+// load, so every workgroup must stay resident at once: PB = 8 keeps the
+// kernel at <= 128 VGPRs (four workgroups per CU).
 // The cache write of an appending call, in the combine's extra grid rows
 // (blockIdx.y >= kHeadsPerGroup), which run beside the merges: the new
 // token's K and V rows of every sequence and kv head go to token
@@ -989,15 +1028,12 @@ __device__ __forceinline__ void copy_new_rows(const AttnArgs& a) {
   }
 }
 
-template <int DT, int D, int KI>
+template <int DT, int D, int KI, int PB>
 __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(AttnArgs a) {
   using E = Elem<DT>;
-  constexpr int D4 = D / 4;                // float4 per query head
-  constexpr int U = 1;                     // pieces loaded together per wave
-  __shared__ float s_m[kHeadsPerGroup - 1][KI][64];
-  __shared__ float s_l[kHeadsPerGroup - 1][KI][64];
-  __shared__ f32x4 s_o[kHeadsPerGroup - 1][KI][64];
-  if (blockIdx.y >= kHeadsPerGroup) {      // uniform: a row of the append's copy
+  constexpr int D4 = D / 4;  // float4 per query head
+  constexpr int NT = 64 * kHeadsPerGroup;
+  if (blockIdx.y >= kHeadsPerGroup) {  // uniform: a row of the append's copy
     copy_new_rows<D>(a);
     return;
   }
@@ -1006,78 +1042,49 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(
   const int b = d.x, grp = d.y, npieces = d.w;
   const int h = grp * kHeadsPerGroup + blockIdx.y;
   if (h >= a.n_kv_heads) return;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int items = a.group * D4;
   const int64_t slot0 = (int64_t)d.z + (int64_t)grp * a.batch + b;
   const int hl0 = blockIdx.y * a.group;  // first query head of h within a slot
-  float m[KI], l[KI];
-  f32x4 o[KI];
 #pragma unroll
   for (int k = 0; k < KI; ++k) {
-    m[k] = -INFINITY;
-    l[k] = 0.f;
-    o[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  for (int s0 = wave; s0 < npieces; s0 += kHeadsPerGroup * U) {
-    float2 ml[U][KI];
-    f32x4 po[U][KI];
+    const int it = (int)threadIdx.x + NT * k;
+    if (it >= items) break;
+    const int64_t pcol = hl0 + it / D4;
+    const int col = 4 * (it % D4);
+    float mx = -INFINITY, lt = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < npieces; s0 += PB) {  // one round for up to PB pieces
+      float2 ml[PB];
+      f32x4 po[PB];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int sp = s0 + u * kHeadsPerGroup;
-#pragma unroll
-      for (int k = 0; k < KI; ++k) {
-        const int it = lane + 64 * k;
-        ml[u][k] = make_float2(-INFINITY, 0.f);
-        if (sp < npieces && it < items) {
-          const int64_t pidx = (slot0 + sp) * a.hpg + hl0 + it / D4;
-          ml[u][k] = a.part_ml[pidx];
-          po[u][k] = *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + 4 * (it % D4));
+      for (int u = 0; u < PB; ++u) {
+        ml[u] = make_float2(-INFINITY, 0.f);
+        po[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (s0 + u < npieces) {  // uniform
+          const int64_t pidx = (slot0 + s0 + u) * a.hpg + pcol;
+          ml[u] = a.part_ml[pidx];
+          po[u] = *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + col);
         }
       }
-    }
+      float mn = mx;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+      for (int u = 0; u < PB; ++u) mn = fmaxf(mn, ml[u].x);
+      if (mn == -INFINITY) continue;  // no readable block yet
+      const float sc = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx - mn);
+      acc *= sc;
+      lt *= sc;
 #pragma unroll
-      for (int k = 0; k < KI; ++k) {
-        if (ml[u][k].x == -INFINITY) continue;  // absent, or a piece with no readable block
-        const float mn = fmaxf(m[k], ml[u][k].x);
-        const float wa = __builtin_amdgcn_exp2f(m[k] - mn);
-        const float wb = __builtin_amdgcn_exp2f(ml[u][k].x - mn);
-        o[k] = o[k] * wa + po[u][k] * wb;
-        l[k] = l[k] * wa + ml[u][k].y * wb;
-        m[k] = mn;
+      for (int u = 0; u < PB; ++u) {
+        // absent, or a piece with no readable block: weight 0
+        const float w = ml[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[u].x - mn);
+        acc += po[u] * w;
+        lt += ml[u].y * w;
       }
-  }
-  if (wave > 0) {
-#pragma unroll
-    for (int k = 0; k < KI; ++k) {
-      s_m[wave - 1][k][lane] = m[k];
-      s_l[wave - 1][k][lane] = l[k];
-      s_o[wave - 1][k][lane] = o[k];
-    }
-  }
-  __syncthreads();
-  if (wave > 0) return;
-#pragma unroll
-  for (int k = 0; k < KI; ++k) {
-    const int it = lane + 64 * k;
-    if (it >= items) continue;
-    float mx = m[k];
-#pragma unroll
-    for (int w = 0; w < kHeadsPerGroup - 1; ++w) mx = fmaxf(mx, s_m[w][k][lane]);
-    const float w0 = m[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[k] - mx);
-    f32x4 acc = o[k] * w0;
-    float lt = l[k] * w0;
-#pragma unroll
-    for (int w = 0; w < kHeadsPerGroup - 1; ++w) {
-      const float mw = s_m[w][k][lane];
-      const float ww = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
-      acc += s_o[w][k][lane] * ww;
-      lt += s_l[w][k][lane] * ww;
+      mx = mn;
     }
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    uint16_t* op = a.out + (int64_t)b * a.out_bstride +
-                   (int64_t)(h * a.group + it / D4) * D + 4 * (it % D4);
+    uint16_t* op = a.out + (int64_t)b * a.out_bstride + (int64_t)(h * a.group) * D +
+                   (int64_t)(it / D4) * D + col;
     *reinterpret_cast<u32x2*>(op) =
         u32x2{E::bits(acc[0] * inv) | (E::bits(acc[1] * inv) << 16),
               E::bits(acc[2] * inv) | (E::bits(acc[3] * inv) << 16)};
@@ -1120,9 +1127,9 @@ bool positions_fit(int64_t chunk, int64_t nblk_max, int64_t n_groups, int64_t n_
   return w_max < (1ll << 31) && w_max * n_groups * n_wg < (1ll << 52);
 }
 
-template <int DT, int D, int KI>
+template <int DT, int D, int KI, int PB>
 int launch_combine(const AttnArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI>),
+  hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI, PB>),
                      dim3(a.n_wg, kHeadsPerGroup + a.copy_rows), dim3(64 * kHeadsPerGroup), 0,
                      stream, a);
   AEGKV_HIP_TRY(hipGetLastError());
@@ -1146,11 +1153,9 @@ int launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
   }
   AEGKV_HIP_TRY(hipGetLastError());
   const int items = a.group * (D / 4);  // <= 16 * D / 4
-  if (items <= 64) return launch_combine<DT, D, 1>(a, stream);
-  if (items <= 128) return launch_combine<DT, D, 2>(a, stream);
-  if (items <= 256) return launch_combine<DT, D, 4>(a, stream);
-  if (items <= 512) return launch_combine<DT, D, 8>(a, stream);
-  return launch_combine<DT, D, 16>(a, stream);
+  if (items <= 64 * kHeadsPerGroup) return launch_combine<DT, D, 1, 8>(a, stream);
+  if (items <= 2 * 64 * kHeadsPerGroup) return launch_combine<DT, D, 2, 8>(a, stream);
+  return launch_combine<DT, D, 4, 8>(a, stream);
 }
 
 }  // namespace

@@ -501,11 +501,13 @@ def bench_gather(args, timer):
     sl_np = wb.seq_lens
     sl = torch.from_numpy(sl_np.astype(np.int32)).to(dev)
     total, max_len = int(sl_np.sum()), int(sl_np.max())
+    # the sequences' start rows, as the step's input preparation provides them
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(sl_np)]), dtype=torch.int32, device=dev)
     outs = {}
 
     def gather(i):
         layer = i % g.n_layers
-        outs[0] = A.gather_tokens(cache, bt, sl, total, max_len, layers=(layer, 1))
+        outs[0] = A.gather_tokens(cache, bt, sl, total, max_len, layers=(layer, 1), cu_seqlens=cu)
 
     gather(0)
     torch.cuda.synchronize()
