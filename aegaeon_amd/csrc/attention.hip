@@ -160,6 +160,7 @@ struct AttnArgs {
   int4* desc;           // [n_wg] cut sequence ending in each workgroup: (b, grp, w0, npieces)
   float* part_o;        // [slots][hpg][D]
   float2* part_ml;      // [slots][hpg] (running max in log2 units, sum)
+  uint32_t ml_bytes, o_bytes;  // sizes of the two partial regions (< 2^31)
   int32_t stage_slots;  // finished pieces a wave holds in LDS (0: stored at once)
   int32_t stage_off;    // byte offset of the staging area in dynamic LDS
   // decode plan (planned launches only): workgroup records, first block ids
@@ -269,39 +270,41 @@ __device__ __forceinline__ void load_block(KVRegs<D>& r, __amdgpu_buffer_rsrc_t 
   for (int c = 0; c < 4; ++c) load_words<KVRegs<D>::VW>(vr, voff + c * row_b, r.v[c]);
 }
 
-// An offset past the end of every range (a block's rows are < 2^31 bytes).
-constexpr uint32_t kOutOfRange = 0x80000000u;
-
 // load_block for a sequence's last block when the call appends: the lanes
 // that hold the new token's row (token noff of the block) read it from the
-// append's input row (knr / vnr, this lane's dims at knoff / vnoff) instead of
-// the cache, whose slot is written only after the attention.  Both loads of a
-// word issue; the lane's offset is out of range in the one it does not use,
-// which then returns zero and reads nothing.
+// append's input rows kn (K, this lane's dims) and vn (V) instead of the
+// cache, whose slot is written only after the attention.  A per-lane choice
+// of address needs global loads (a buffer range is uniform over the wave);
+// two buffer loads per word with an OR of their results doubled the
+// registers in flight and spilled.  kh / vh are this lane's K / V addresses
+// in block 0 and off the block's offset; a pipeline refill past the range
+// re-reads the range's last block.
+template <int NW>
+__device__ __forceinline__ void load_words_global(const uint16_t* p, uint32_t* w) {
+  if constexpr (NW == 2) {
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    w[0] = v.x; w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) {
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 8 * i));
+      w[4 * i + 0] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  }
+}
 template <int D>
-__device__ __forceinline__ void load_block_new(KVRegs<D>& r, __amdgpu_buffer_rsrc_t kr,
-                                               __amdgpu_buffer_rsrc_t vr, uint32_t koff,
-                                               uint32_t voff, uint32_t row_b, int noff,
-                                               __amdgpu_buffer_rsrc_t knr,
-                                               __amdgpu_buffer_rsrc_t vnr, uint32_t knoff,
-                                               uint32_t vnoff) {
+__device__ __forceinline__ void load_block_new(KVRegs<D>& r, const uint16_t* kh,
+                                               const uint16_t* vh, int64_t off, int64_t row,
+                                               int noff, const uint16_t* kn, const uint16_t* vn) {
   const int lane = threadIdx.x & 63;
   const int j = lane & 15, g = lane >> 4;
-  const bool kn = j == noff;
-  const uint32_t kc_at = kn ? kOutOfRange : koff, kn_at = kn ? knoff : kOutOfRange;
+  const uint16_t* kp = j == noff ? kn : kh + off;
 #pragma unroll
   for (int ks = 0; ks < KVRegs<D>::KS; ++ks)
-    r.k[ks] = __builtin_amdgcn_raw_buffer_load_b128(kr, kc_at + 64 * ks, 0, kNt) |
-              __builtin_amdgcn_raw_buffer_load_b128(knr, kn_at + 64 * ks, 0, kNt);
+    r.k[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 32 * ks));
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const bool vn = 4 * g + c == noff;
-    uint32_t wc[KVRegs<D>::VW], wn[KVRegs<D>::VW];
-    load_words<KVRegs<D>::VW>(vr, vn ? kOutOfRange : voff + c * row_b, wc);
-    load_words<KVRegs<D>::VW>(vnr, vn ? vnoff : kOutOfRange, wn);
-#pragma unroll
-    for (int w = 0; w < KVRegs<D>::VW; ++w) r.v[c][w] = wc[w] | wn[w];
-  }
+  for (int c = 0; c < 4; ++c)
+    load_words_global<KVRegs<D>::VW>(4 * g + c == noff ? vn : vh + off + c * row, r.v[c]);
 }
 
 // Softmax update and P.V for one block whose first token is `tok0`; `len` is
@@ -485,8 +488,9 @@ __device__ __forceinline__ void get_record(const uint8_t* rec, f32x4* acc, float
 // sequence and the start of the next.  A sequence piece that ends costs its
 // output stores and the switch to the next sequence, whose query was loaded
 // when the previous switch happened.  Inside the loop every K/V load is
-// issued unconditionally: a refill past the range, and an unreadable block
-// id, load through an empty buffer range, which reads no memory (re-reading
+// issued unconditionally: without an append, a refill past the range and an
+// unreadable block id load through an empty buffer range, which reads no
+// memory (re-reading
 // the range's last block instead cost 4% more HBM traffic on the
 // Qwen2.5-7B batch and 12% on the Yi-1.5-9B one, as the non-temporal lines
 // were gone from L2).  Block ids come 64 items at a time, one per lane, with
@@ -635,23 +639,22 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   // An appending call swaps the new token's row into each sequence's last
   // block by lane-wise address selects (no branch around the loads, so the
   // compiler's wait counts stay exact).
-  // `valid`: the item is in the range (a refill past its end reads nothing)
+  // `valid`: the item is in the range (a refill past its end reads nothing;
+  // with an append, it re-reads the range's last block)
+  const uint16_t* kh = FUSED ? a.kc + (int64_t)h * D + (int64_t)j * row + 8 * g : nullptr;
+  const uint16_t* vh = FUSED ? a.vc + (int64_t)h * D + (int64_t)(4 * g) * row + DPL * j : nullptr;
+  const uint16_t* kn_lane = FUSED ? a.knew + (int64_t)h * D + 8 * g : nullptr;
+  const uint16_t* vn_lane = FUSED ? a.vnew + (int64_t)h * D + DPL * j : nullptr;
   auto load_item = [&](KVRegs<D>& r, int id, int tag, bool valid) {
-    const bool ok = valid && id >= 0;
     const int64_t off = (int64_t)max(id, 0) * a.blk_stride;
-    const auto kr = byte_range(reinterpret_cast<const uint8_t*>(a.kc + off), ok ? blk_b : 0u);
-    const auto vr = byte_range(reinterpret_cast<const uint8_t*>(a.vc + off), ok ? blk_b : 0u);
     if constexpr (FUSED) {
-      const int b = max(tag, 0) >> 4, noff = tag < 0 ? -1 : (tag & (kBlockSize - 1));
-      const bool nw = valid && tag >= 0;
-      const auto knr = byte_range(
-          reinterpret_cast<const uint8_t*>(a.knew + (int64_t)b * a.knew_bstride), nw ? row_b : 0u);
-      const auto vnr = byte_range(
-          reinterpret_cast<const uint8_t*>(a.vnew + (int64_t)b * a.vnew_bstride), nw ? row_b : 0u);
-      load_block_new<D>(r, kr, vr, koff, voff, row_b, noff, knr, vnr,
-                        (uint32_t)(((int64_t)h * D + 8 * g) * 2),
-                        (uint32_t)(((int64_t)h * D + DPL * j) * 2));
+      const int b = tag >> 4, noff = tag < 0 ? -1 : (tag & (kBlockSize - 1));
+      load_block_new<D>(r, kh, vh, off, row, noff, kn_lane + (int64_t)b * a.knew_bstride,
+                        vn_lane + (int64_t)b * a.vnew_bstride);
     } else {
+      const bool ok = valid && id >= 0;
+      const auto kr = byte_range(reinterpret_cast<const uint8_t*>(a.kc + off), ok ? blk_b : 0u);
+      const auto vr = byte_range(reinterpret_cast<const uint8_t*>(a.vc + off), ok ? blk_b : 0u);
       load_block<D>(r, kr, vr, koff, voff, row_b);
     }
   };
@@ -991,8 +994,10 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
 // nine-piece sequence against 1.7 us for two; this version measured 2.4 us
 // per layer faster on the Qwen2.5-7B batch and 1.9 us on the Yi-1.5-9B one.)
 // Most of the grid's workgroups hold no task and exit after the descriptor
-// load, so every workgroup must stay resident at once: PB = 8 keeps the
-// kernel at <= 128 VGPRs (four workgroups per CU).
+// load, so every workgroup must stay resident at once (four per CU): the
+// pieces are raw buffer loads whose piece stride is a scalar offset, which
+// keeps PB = 12 at ~110 VGPRs (PB = 16 measured 1 us slower on the
+// Yi-1.5-9B batch, whose longest sequences have 10-15 pieces; 8 the same).
 // The cache write of an appending call, in the combine's extra grid rows
 // (blockIdx.y >= kHeadsPerGroup), which run beside the merges: the new
 // token's K and V rows of every sequence and kv head go to token
@@ -1045,12 +1050,19 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(
   const int items = a.group * D4;
   const int64_t slot0 = (int64_t)d.z + (int64_t)grp * a.batch + b;
   const int hl0 = blockIdx.y * a.group;  // first query head of h within a slot
+  // the partials as raw buffers: a piece's offset is a uniform (scalar)
+  // stride, so the PB loads of a round share one vector offset per thread
+  // (the host keeps both regions below 2^31 bytes)
+  const auto mlr = byte_range(reinterpret_cast<const uint8_t*>(a.part_ml), a.ml_bytes);
+  const auto por = byte_range(reinterpret_cast<const uint8_t*>(a.part_o), a.o_bytes);
+  const uint32_t ml_step = (uint32_t)a.hpg * 8u, o_step = (uint32_t)a.hpg * D * 4u;
 #pragma unroll
   for (int k = 0; k < KI; ++k) {
     const int it = (int)threadIdx.x + NT * k;
     if (it >= items) break;
-    const int64_t pcol = hl0 + it / D4;
+    const int64_t pidx0 = slot0 * a.hpg + hl0 + it / D4;
     const int col = 4 * (it % D4);
+    const uint32_t ml_off = (uint32_t)(pidx0 * 8), o_off = (uint32_t)((pidx0 * D + col) * 4);
     float mx = -INFINITY, lt = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < npieces; s0 += PB) {  // one round for up to PB pieces
@@ -1061,9 +1073,12 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(
         ml[u] = make_float2(-INFINITY, 0.f);
         po[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (s0 + u < npieces) {  // uniform
-          const int64_t pidx = (slot0 + s0 + u) * a.hpg + pcol;
-          ml[u] = a.part_ml[pidx];
-          po[u] = *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + col);
+          const uint32_t sp = (uint32_t)(s0 + u);
+          const u32x2 mw = __builtin_amdgcn_raw_buffer_load_b64(mlr, ml_off, sp * ml_step, 0);
+          ml[u] = make_float2(__uint_as_float(mw.x), __uint_as_float(mw.y));
+          const u32x4 ow = __builtin_amdgcn_raw_buffer_load_b128(por, o_off, sp * o_step, 0);
+          po[u] = f32x4{__uint_as_float(ow.x), __uint_as_float(ow.y), __uint_as_float(ow.z),
+                        __uint_as_float(ow.w)};
         }
       }
       float mn = mx;
@@ -1153,9 +1168,9 @@ int launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
   }
   AEGKV_HIP_TRY(hipGetLastError());
   const int items = a.group * (D / 4);  // <= 16 * D / 4
-  if (items <= 64 * kHeadsPerGroup) return launch_combine<DT, D, 1, 8>(a, stream);
-  if (items <= 2 * 64 * kHeadsPerGroup) return launch_combine<DT, D, 2, 8>(a, stream);
-  return launch_combine<DT, D, 4, 8>(a, stream);
+  if (items <= 64 * kHeadsPerGroup) return launch_combine<DT, D, 1, 12>(a, stream);
+  if (items <= 2 * 64 * kHeadsPerGroup) return launch_combine<DT, D, 2, 12>(a, stream);
+  return launch_combine<DT, D, 4, 12>(a, stream);
 }
 
 }  // namespace
@@ -1258,6 +1273,9 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
   }
   a.part_ml = reinterpret_cast<float2*>(ws + lay.desc_bytes);
   a.part_o = reinterpret_cast<float*>(ws + lay.desc_bytes + lay.ml_bytes);
+  if (lay.ml_bytes >= (1ll << 31) || lay.o_bytes >= (1ll << 31)) return AEGKV_ERR_UNSUPPORTED;
+  a.ml_bytes = (uint32_t)lay.ml_bytes;
+  a.o_bytes = (uint32_t)lay.o_bytes;
   hipStream_t st = (hipStream_t)stream;
   const bool bf = dtype == AEGKV_DTYPE_BF16;
   DeviceState* ds = nullptr;
