@@ -9,7 +9,14 @@
 // to keys j <= i of the same sequence (all of them when not causal).
 //
 // Work: a workgroup of four waves takes 128 queries of one head of one
-// sequence; wave w owns queries [32w, 32w + 32).  Workgroups are numbered with
+// sequence; wave w owns queries [32w, 32w + 32).  The (sequence, query head)
+// units, in that order (so the query heads of one kv head are neighbours), are
+// split into kXcds contiguous runs, one per XCD: the hardware deals
+// workgroup i to XCD i % kXcds, and workgroup i = s * kXcds + x takes the
+// s-th job of XCD x's run.  Every query tile of a unit then runs on one XCD,
+// whose L2 keeps that sequence's K and V for all of them (round-robin jobs
+// put each kv head's 1 MiB of K/V of a 2048-token prompt in every XCD's L2,
+// 16 MiB per 4 MiB L2 for 4 x 2048 tokens).  Within an XCD the jobs run with
 // the query tile slowest, in decreasing order, so the most expensive tiles
 // (the last of each sequence) are dispatched first; two fit on a CU.  (A
 // persistent grid dealing the same jobs in snake order measured 5% slower on
@@ -47,6 +54,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPfThreads = 256;
+constexpr int kXcds = 8;                     // XCDs of an MI355X (gfx950)
 constexpr int kPfQTile = 128;                // queries per workgroup
 constexpr int kPfKTile = 64;                 // keys per step
 constexpr int kVtPitch = kPfKTile * 2 + 16;  // bytes per row of V^T in LDS
@@ -104,6 +112,7 @@ struct PrefillArgs {
   const int32_t* cu_seqlens;                   // [batch + 1], device
   int64_t total_tokens;
   int32_t batch, n_q_heads, group, max_seqlen, n_qtiles, causal;
+  int32_t n_units;                             // batch * n_q_heads
   float scale_log2;                            // softmax scale * log2(e), > 0
 };
 
@@ -342,11 +351,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(Prefil
   constexpr int V_BYTES = D * kVtPitch;
   // two K stages, then two V^T stages
   __shared__ __align__(16) uint8_t lds[2 * K_BYTES + 2 * V_BYTES];
-  const int hb = a.n_q_heads * a.batch;
-  const int job = blockIdx.x;
-  const int tile = a.n_qtiles - 1 - job / hb;
-  const int h = (job % hb) / a.batch;
-  const int b = job % a.batch;
+  // XCD x's run of units [u0, u1); its s-th job: tile n_qtiles-1 - s / c,
+  // unit u0 + s % c (all uniform over the workgroup)
+  const int x = (int)(blockIdx.x % kXcds), sj = (int)(blockIdx.x / kXcds);
+  const int u0 = (int)((int64_t)a.n_units * x / kXcds);
+  const int c = (int)((int64_t)a.n_units * (x + 1) / kXcds) - u0;
+  if (c == 0 || sj >= a.n_qtiles * c) return;
+  const int tile = a.n_qtiles - 1 - sj / c;
+  const int unit = u0 + sj % c;
+  const int b = unit / a.n_q_heads;
+  const int h = unit % a.n_q_heads;
   int64_t s0 = a.cu_seqlens[b], s1 = a.cu_seqlens[b + 1];
   s0 = min(max(s0, (int64_t)0), a.total_tokens);
   s1 = min(max(s1, s0), a.total_tokens);
@@ -394,9 +408,10 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
       q_token_stride % 8 || k_token_stride % 8 || v_token_stride % 8 || out_token_stride % 8)
     return AEGKV_ERR_MISALIGNED;
   const int64_t n_qtiles = ((int64_t)max_seqlen + kPfQTile - 1) / kPfQTile;
-  const int64_t n_jobs = n_qtiles * n_q_heads * batch;
-  if (n_jobs > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
-  const int64_t grid = n_jobs;
+  const int64_t n_units = (int64_t)n_q_heads * batch;
+  // kXcds runs of at most ceil(n_units / kXcds) units each
+  const int64_t grid = kXcds * n_qtiles * ((n_units + kXcds - 1) / kXcds);
+  if (grid > INT32_MAX || n_units * n_qtiles > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
 
   PrefillArgs a;
   a.q = static_cast<const uint8_t*>(q);
@@ -414,6 +429,7 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
   a.group = n_q_heads / n_kv_heads;
   a.max_seqlen = max_seqlen;
   a.n_qtiles = (int32_t)n_qtiles;
+  a.n_units = (int32_t)n_units;
   a.causal = causal ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
   const uint32_t g = (uint32_t)grid;
