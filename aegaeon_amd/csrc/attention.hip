@@ -14,9 +14,10 @@
 // whose pieces write fp32 partials (unnormalised O, running max in log2
 // units, sum).  A workgroup's range can end at most one cut sequence (a cut
 // sequence ending inside a range began before it, i.e. at the range's start),
-// so each workgroup leaves a 16-byte descriptor of that sequence (or none),
-// and a second kernel, one workgroup per descriptor and kv head, merges its
-// pieces with log-sum-exp weights.  A sequence held by one workgroup is
+// so each workgroup leaves a 16-byte descriptor of that sequence (or none;
+// a plan instead holds one per sequence when sequences are fewer than
+// workgroups), and a second kernel, one workgroup per descriptor and kv head,
+// merges its pieces with log-sum-exp weights.  A sequence held by one workgroup is
 // normalised and written directly.  (Merging in the main kernel by the last
 // piece to arrive measured slower every way it was built: with device-scope
 // release fences, which write back the XCD's L2, 2x; with write-through
@@ -178,7 +179,17 @@ struct AttnArgs {
   const uint16_t* vnew;
   int64_t knew_bstride, vnew_bstride;  // elements
   int32_t copy_rows;                   // combine grid rows that copy new rows
+  int32_t n_desc;                      // merge descriptors (the combine grid's width)
 };
+
+// A plan indexes the merge descriptors by (kv-head group, sequence) when there
+// are fewer of those than workgroups, so that the combine grid has one
+// workgroup per sequence instead of one per main-kernel workgroup (the
+// Yi-1.5-9B batch: 64 against 256, of which 61 cut); otherwise, and without a
+// plan, by the workgroup holding the sequence's last piece.
+inline bool desc_per_sequence(int64_t batch, int64_t n_groups, int64_t n_wg) {
+  return batch * n_groups < n_wg;
+}
 
 // Decode plan, in one device buffer: per main-kernel workgroup a record of 8
 // int32 (first kv-head group or -1 for an idle workgroup, last group, first
@@ -883,6 +894,7 @@ struct PlanArgs {
   int32_t max_seq_len;
   int32_t n_groups;
   int32_t n_wg;
+  int32_t desc_per_seq;  // desc indexed by grp * batch + b (else by workgroup)
   int32_t* wg;
   int4* desc;
   int32_t* first;
@@ -935,7 +947,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
     int32_t* rec = p.wg + (int64_t)w * kPlanRecord;
     if (w >= n_act) {
       rec[0] = -1;
-      p.desc[w] = make_int4(-1, 0, 0, 0);
+      if (!p.desc_per_seq) p.desc[w] = make_int4(-1, 0, 0, 0);
       continue;
     }
     const Range r = range_of(w);
@@ -947,12 +959,26 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
     rec[5] = seq_at(s_cum, p.batch, 0);  // first non-empty sequence
     rec[6] = 0;
     rec[7] = 0;
+    if (p.desc_per_seq) continue;
     // the range's first piece is the only one that can end a cut sequence
     const int64_t pbase = (int64_t)r.gf * W;
     const int64_t w0 = owner_of(pbase + s_cum[r.b0] + kSegmentCost, total, n_act);
     const int64_t w1 = owner_of(pbase + s_cum[r.b0 + 1] - 1, total, n_act);
     p.desc[w] = (w0 != w1 && w1 == (int64_t)w) ? make_int4(r.b0, r.gf, (int)w0, (int)(w1 - w0 + 1))
                                                : make_int4(-1, 0, 0, 0);
+  }
+  if (p.desc_per_seq) {  // one descriptor per (group, sequence): cut or not
+    for (int e = gtid; e < p.n_groups * p.batch; e += gsz) {
+      const int grp = e / p.batch, b = e % p.batch;
+      int4 d = make_int4(-1, 0, 0, 0);
+      if (s_bcum[b + 1] > s_bcum[b]) {
+        const int64_t pbase = (int64_t)grp * W;
+        const int64_t w0 = owner_of(pbase + s_cum[b] + kSegmentCost, total, n_act);
+        const int64_t w1 = owner_of(pbase + s_cum[b + 1] - 1, total, n_act);
+        if (w0 != w1) d = make_int4(b, grp, (int)w0, (int)(w1 - w0 + 1));
+      }
+      p.desc[e] = d;
+    }
   }
   auto id_of = [&](int i) -> int32_t {
     const int b = seq_at(s_bcum, p.batch, i);
@@ -981,9 +1007,8 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
                     : -1;
 }
 
-// Merge the pieces of the cut sequence whose last block workgroup
-// blockIdx.x of the main kernel held (none: nothing to do), for kv head
-// grp * 4 + blockIdx.y:
+// Merge the pieces of the cut sequence that descriptor blockIdx.x names
+// (none: nothing to do), for kv head grp * 4 + blockIdx.y:
 //   out = sum_s w_s o_s / sum_s w_s l_s,  w_s = 2^(m_s - max m).
 // The kv head's G query heads x D/4 float4 columns are "items", one per
 // thread (KI per thread past 256 items); a thread loads the (m, l) and o of
@@ -1145,7 +1170,7 @@ bool positions_fit(int64_t chunk, int64_t nblk_max, int64_t n_groups, int64_t n_
 template <int DT, int D, int KI, int PB>
 int launch_combine(const AttnArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI, PB>),
-                     dim3(a.n_wg, kHeadsPerGroup + a.copy_rows), dim3(64 * kHeadsPerGroup), 0,
+                     dim3(a.n_desc, kHeadsPerGroup + a.copy_rows), dim3(64 * kHeadsPerGroup), 0,
                      stream, a);
   AEGKV_HIP_TRY(hipGetLastError());
   return AEGKV_OK;
@@ -1259,7 +1284,9 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
   a.knew_bstride = nr.key_bstride;
   a.vnew_bstride = nr.value_bstride;
   a.copy_rows = 0;
+  a.n_desc = n_wg;
   if (plan) {
+    if (desc_per_sequence(batch, n_groups, n_wg)) a.n_desc = batch * n_groups;
     const PlanLayout pl = plan_layout(batch, n_wg, nblk_max);
     if (plan_bytes < (uint64_t)pl.total) return AEGKV_ERR_INVALID_ARG;
     if (!aligned16(plan)) return AEGKV_ERR_MISALIGNED;
@@ -1294,7 +1321,7 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
       a.vnew = static_cast<const uint16_t*>(nr.value) + (int64_t)c * nr.value_bstride;
       // enough combine rows that each copy lane moves about one 16-byte chunk
       const int64_t chunks = (int64_t)a.batch * n_kv_heads * 2 * (head_dim / 8);
-      const int64_t per_row = (int64_t)n_wg * 64 * kHeadsPerGroup;
+      const int64_t per_row = (int64_t)a.n_desc * 64 * kHeadsPerGroup;
       a.copy_rows = (int32_t)std::min<int64_t>(64, std::max<int64_t>(1, (chunks + per_row - 1) / per_row));
     }
     const size_t lds = lds_bytes(a, ds->max_lds);
@@ -1493,13 +1520,15 @@ int aegkv_paged_decode_plan(const int32_t* block_tables, int32_t max_blocks,
   p.max_seq_len = max_seq_len;
   p.n_groups = (n_kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
   p.n_wg = n_wg;
+  p.desc_per_seq = desc_per_sequence(batch, p.n_groups, n_wg) ? 1 : 0;
   p.wg = reinterpret_cast<int32_t*>(pb + pl.wg);
   p.desc = reinterpret_cast<int4*>(pb + pl.desc);
   p.first = reinterpret_cast<int32_t*>(pb + pl.first);
   p.last = reinterpret_cast<int32_t*>(pb + pl.last);
   p.ids = reinterpret_cast<int32_t*>(pb + pl.ids);
   p.tags = reinterpret_cast<int32_t*>(pb + pl.tags);
-  const int64_t work = std::max<int64_t>((int64_t)n_wg * 64, (int64_t)batch * nblk_max);
+  const int64_t work = std::max<int64_t>(std::max<int64_t>((int64_t)n_wg * 64, (int64_t)batch * nblk_max),
+                                         (int64_t)batch * p.n_groups);
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(1024, (work + 255) / 256));
   hipLaunchKernelGGL(decode_plan_kernel, dim3(grid), dim3(64 * kHeadsPerGroup),
                      (size_t)(3 * batch + 2) * sizeof(int32_t), (hipStream_t)stream, p);
