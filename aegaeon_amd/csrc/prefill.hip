@@ -8,22 +8,7 @@
 // holds tokens [cu_seqlens[b], cu_seqlens[b+1]); query i of a sequence attends
 // to keys j <= i of the same sequence (all of them when not causal).
 //
-// Work: a workgroup of four waves takes 128 queries of one head of one
-// sequence; wave w owns queries [32w, 32w + 32).  The (sequence, query head)
-// units, in that order (so the query heads of one kv head are neighbours), are
-// split into kXcds contiguous runs, one per XCD: the hardware deals
-// workgroup i to XCD i % kXcds, and workgroup i = s * kXcds + x takes the
-// s-th job of XCD x's run.  Every query tile of a unit then runs on one XCD,
-// whose L2 keeps that sequence's K and V for all of them (round-robin jobs
-// put each kv head's 1 MiB of K/V of a 2048-token prompt in every XCD's L2,
-// 16 MiB per 4 MiB L2 for 4 x 2048 tokens).  Within an XCD the jobs run with
-// the query tile slowest, in decreasing order, so the most expensive tiles
-// (the last of each sequence) are dispatched first; two fit on a CU.  (A
-// persistent grid dealing the same jobs in snake order measured 5% slower on
-// 4 x 2048 tokens and 60% slower on ragged batches, whose short sequences
-// leave most high-tile jobs empty.)
-//
-// Per 64-key tile, staged in LDS by the whole workgroup (two stages):
+// Per 64-key tile and 32-query block of a wave:
 //   S^T[64 keys x 32 queries] = K[64 x D] . Q^T[D x 32]   2 x D/16 MFMA 32x32x16
 //     (A = K rows from LDS, B = the wave's queries, held in registers);
 //   online softmax in fp32 in the exp2 domain: lane l holds query l & 31 and
@@ -32,10 +17,47 @@
 //   O^T[D x 32] += V^T[D x 64] . P^T[64 x 32]             D/32 x 4 MFMA 32x32x16
 //     with P rounded to 16 bits (as FlashAttention does) and taken straight
 //     from the S^T accumulators: elements 8j .. 8j+7 of a lane are the keys of
-//     k-step j, so V^T is stored in LDS with the 4-key quads of every 16 keys
-//     in the order 0, 2, 1, 3, and each MFMA operand is one 16-byte LDS read.
+//     k-step j, which are keys {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3} of
+//     the step's 16 (hh = l / 32), so V^T's A operand holds those keys.
 // Lazy rescaling as in the decode kernel: the reference max moves only when a
 // tile's max exceeds it by more than 8 (log2 units).
+//
+// Two kernels share that arithmetic (their outputs are bit-identical); the
+// host picks one by the batch's longest prompt:
+//
+// Long prompts (max_seqlen > kLongPrompt): ping-pong.  A workgroup of eight
+// waves takes 256 queries of one head and fills a CU; waves w and w + 4 share
+// a SIMD, and the two halves of the workgroup run opposite phases between
+// workgroup barriers.  Per key tile j a wave runs a matrix phase (S_j and the
+// previous tile's O += V_{j-1}^T . P_{j-1}, 32 MFMAs at D = 128) and then a
+// softmax phase (the VALU work that turns S_j into P_j); waves 4-7 start one
+// phase later than waves 0-3, so on every SIMD one wave feeds the matrix core
+// while the other runs its softmax.  K and V go from HBM straight into LDS
+// (buffer loads with the LDS bit, no registers), V untransposed, and the
+// P.V operands are read with gfx950's transposing LDS reads.  Since only one
+// wave per SIMD is ever in its softmax, the partner lanes exchange their
+// maxima with v_permlane32_swap instead of an LDS round trip.
+//
+// Short prompts: two workgroups of four waves per CU, each taking 128 queries;
+// K and V are staged through registers (V transposed on the way into LDS) and
+// the two workgroups overlap each other's softmax and matrix work unordered.
+// (With short prompts the ping-pong workgroup's start-up and its larger
+// causal diagonal cost more than the phase overlap gains: 8 x 1024 tokens
+// 112.6 against 109.0 us, 16 x 512 90.1 against 78.5 us; from 2048 tokens on it
+// is faster: 4 x 2048 cache-cold 174.0 against 181.0 us, 2 x 4096 269.5
+// against 303.7 us, 1 x 8192 544.7 against 627.3 us.)
+//
+// Work order, both kernels: the (sequence, query head) units, in that order
+// (so the query heads of one kv head are neighbours), are split into kXcds
+// contiguous runs, one per XCD: the hardware deals workgroup i to XCD
+// i % kXcds, and workgroup i = s * kXcds + x takes the s-th job of XCD x's
+// run.  Every query tile of a unit then runs on one XCD, whose L2 keeps that
+// sequence's K and V for all of them.  Within an XCD the jobs run with the
+// query tile slowest, in decreasing order, so the most expensive tiles (the
+// last of each sequence) are dispatched first.  (A persistent grid dealing the
+// same jobs in snake order measured 5% slower on 4 x 2048 tokens and 60%
+// slower on ragged batches, whose short sequences leave most high-tile jobs
+// empty.)
 #include <algorithm>
 #include <cmath>
 
@@ -52,13 +74,22 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kPfThreads = 256;
 constexpr int kXcds = 8;                     // XCDs of an MI355X (gfx950)
-constexpr int kPfQTile = 128;                // queries per workgroup
 constexpr int kPfKTile = 64;                 // keys per step
-constexpr int kVtPitch = kPfKTile * 2 + 16;  // bytes per row of V^T in LDS
 constexpr float kPfRescaleSlack = 8.f;
+constexpr int kLongPrompt = 1536;            // longer prompts take the ping-pong kernel
+// short-prompt kernel: four waves, 128 queries, V^T staged transposed
+constexpr int kShortThreads = 256;
+constexpr int kShortQTile = 128;
+constexpr int kVtPitch = kPfKTile * 2 + 16;  // bytes per row of V^T in LDS
+// ping-pong kernel: eight waves, 256 queries
+constexpr int kLongWaves = 8;
+constexpr int kLongThreads = 64 * kLongWaves;
+constexpr int kLongQTile = 32 * kLongWaves;
 
 template <int DT>
 struct PfOps;
@@ -116,23 +147,195 @@ struct PrefillArgs {
   float scale_log2;                            // softmax scale * log2(e), > 0
 };
 
-// Queries [q0, q0 + 128) of head h of the sequence at token s0 with len
-// tokens.
+// The wave's state for its 32 queries: lane (col = l & 31, hh = l / 32) holds
+// query q0 + col and, of the O^T accumulators, head dims 32 db + 8 g + 4 hh ..
+// + 3 in element 4 g .. 4 g + 3 of o[db].
 template <int DT, int D>
-__device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, int h, int64_t s0,
-                                            int len, int q0) {
+struct WaveState {
+  static constexpr int KS = D / 16;  // k-steps of K.Q^T
+  static constexpr int DB = D / 32;  // 32-row blocks of O^T
+  u32x4 qv[KS];                      // Q^T operand: dims 16 ks + 8 hh .. +7
+  f32x16 o[DB];
+  float m, lsum;
+
+  __device__ __forceinline__ void init(const PrefillArgs& a, int h, int64_t s0, int len, int qi,
+                                       int hh) {
+    const uint8_t* qp =
+        a.q + (s0 + min(qi, len - 1)) * a.q_tok_b + ((int64_t)h * D + 8 * hh) * 2;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)  // queries past the end: 0
+      qv[ks] = qi < len ? *reinterpret_cast<const u32x4*>(qp + 32 * ks) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+    m = -INFINITY;
+    lsum = 0.f;
+  }
+
+  // S^T of a 64-key tile from K rows at kp (pitch KPITCH bytes, this lane's
+  // row and 16-byte column already added); the two 32-key blocks alternate so
+  // that neighbouring MFMAs are independent.  `ahead` LDS reads are kept in
+  // flight ahead of the MFMA that uses them.
+  template <int KPITCH, int AHEAD>
+  __device__ __forceinline__ void qk(const uint8_t* kp, f32x16 (&s)[2]) const {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+        s[sb] = PfOps<DT>::mfma(*reinterpret_cast<const u32x4*>(kp + 32 * sb * KPITCH + 32 * ks),
+                                qv[ks], s[sb]);
+    if (AHEAD > 0) {
+      __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);  // LDS reads
+#pragma unroll
+      for (int i = 0; i < 2 * KS - AHEAD; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // the next read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
+    }
+  }
+
+  // -inf where a key of the tile at k0 is past the end or (causal) after the
+  // query; only the tiles that reach past the wave's first query wq0 or the
+  // end need it
+  __device__ __forceinline__ void mask(f32x16 (&s)[2], int k0, int wq0, int qi, int len,
+                                       int causal, int hh) const {
+    if ((causal && k0 + kPfKTile - 1 > wq0) || k0 + kPfKTile > len) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kv = k0 + 32 * sb + 8 * (i >> 2) + 4 * hh + (i & 3);
+          const bool ok = kv < len && (!causal || kv <= qi);
+          s[sb][i] = ok ? s[sb][i] : -INFINITY;
+        }
+    }
+  }
+
+  // online softmax of a masked S^T tile into the P^T operands of its four
+  // 16-key steps (kSwap: the partner lanes exchange their maxima with
+  // v_permlane32_swap, see below)
+  template <bool kSwap>
+  __device__ __forceinline__ void softmax(f32x16 (&s)[2], u32x4 (&pb)[4], float scale_log2) {
+    float b4[4];  // raw-score max (the scale is positive) over four chains
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x16& x = s[c >> 1];
+      const int e = 8 * (c & 1);
+      b4[c] = max3(max3(x[e], x[e + 1], x[e + 2]), max3(x[e + 3], x[e + 4], x[e + 5]),
+                   max3(x[e + 6], x[e + 7], x[e + 7]));
+    }
+    float bm = max3(max3(b4[0], b4[1], b4[2]), b4[3], b4[3]);
+    // the partner lane's max (same query)
+    if (kSwap) {
+      // exchanged between the wave's halves in registers: one
+      // v_permlane32_swap instead of an LDS round trip.  Only where no other
+      // wave of the SIMD can run it at the same time: with two waves of
+      // unsynchronised workgroups per SIMD, both in their softmax, it gave
+      // run-to-run different outputs (also with wait states around it, and
+      // never with one wave per SIMD).
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm),
+                                                       false, false);
+      bm = fmaxf(fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])), bm) * scale_log2;
+    } else {
+      const float pm = __shfl_xor(bm, 32);
+      bm = max3(bm, pm, pm) * scale_log2;
+    }
+    if (__builtin_amdgcn_ballot_w64(bm > m + kPfRescaleSlack)) {
+      const float mn = fmaxf(m, bm);
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 while m = -inf
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+      m = mn;
+    }
+    const float nms = m == -INFINITY ? 0.f : -m;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int sb = kk >> 1, base = 8 * (kk & 1);
+      uint32_t pw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p0 =
+            __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][base + 2 * j], scale_log2, nms));
+        const float p1 =
+            __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][base + 2 * j + 1], scale_log2, nms));
+        lsum += p0 + p1;
+        pw[j] = PfOps<DT>::pack(p0, p1);
+      }
+      pb[kk] = u32x4{pw[0], pw[1], pw[2], pw[3]};
+    }
+  }
+
+  // normalise and store the lane's outputs (queries past the end: none)
+  __device__ __forceinline__ void store(const PrefillArgs& a, int h, int64_t s0, int len, int qi,
+                                        int hh) {
+    // both waves of a SIMD may run this at once: no v_permlane32_swap here
+    const float lt = lsum + __shfl_xor(lsum, 32);
+    if (qi < len) {
+      const float inv = 1.f / lt;
+      uint8_t* op = a.out + (s0 + qi) * a.o_tok_b + ((int64_t)h * D + 4 * hh) * 2;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x16& r = o[db];
+          *reinterpret_cast<u32x2*>(op + (32 * db + 8 * g) * 2) =
+              u32x2{PfOps<DT>::pack(r[4 * g] * inv, r[4 * g + 1] * inv),
+                    PfOps<DT>::pack(r[4 * g + 2] * inv, r[4 * g + 3] * inv)};
+        }
+    }
+  }
+};
+
+// Uniform job of workgroup blockIdx.x for query tiles of qtile queries:
+// returns false when the tile is empty.
+__device__ __forceinline__ bool pick_job(const PrefillArgs& a, int qtile, int& h, int64_t& s0,
+                                         int& len, int& q0) {
+  // XCD x's run of units [u0, u0 + c); its s-th job: tile n_qtiles-1 - s / c,
+  // unit u0 + s % c
+  const int x = (int)(blockIdx.x % kXcds), sj = (int)(blockIdx.x / kXcds);
+  const int u0 = (int)((int64_t)a.n_units * x / kXcds);
+  const int c = (int)((int64_t)a.n_units * (x + 1) / kXcds) - u0;
+  if (c == 0 || sj >= a.n_qtiles * c) return false;
+  const int tile = a.n_qtiles - 1 - sj / c;
+  const int unit = u0 + sj % c;
+  const int b = unit / a.n_q_heads;
+  h = unit % a.n_q_heads;
+  int64_t s1 = a.cu_seqlens[b + 1];
+  s0 = a.cu_seqlens[b];
+  s0 = min(max(s0, (int64_t)0), a.total_tokens);
+  s1 = min(max(s1, s0), a.total_tokens);
+  len = (int)min(s1 - s0, (int64_t)a.max_seqlen);
+  q0 = tile * qtile;
+  return q0 < len;
+}
+
+// ---------------------------------------------------------------- short prompts
+// Queries [q0, q0 + 128) of head h of the sequence at token s0 with len
+// tokens; K and V tiles staged through registers, two stages each in LDS (V
+// transposed, the 4-key quads of every 16 keys in the order 0, 2, 1, 3, so each
+// P.V operand is one 16-byte LDS read).
+template <int DT, int D>
+__device__ __forceinline__ void attend_short(const PrefillArgs& a, uint8_t* lds, int h, int64_t s0,
+                                             int len, int q0) {
   using E = PfOps<DT>;
+  using W = WaveState<DT, D>;
   constexpr int KPITCH = D * 2 + 16;            // bytes per K row in LDS
   constexpr int K_BYTES = kPfKTile * KPITCH;
   constexpr int V_BYTES = D * kVtPitch;
-  constexpr int KS = D / 16;                    // k-steps of K.Q^T
-  constexpr int DB = D / 32;                    // 32-row blocks of O^T
+  constexpr int DB = W::DB;
   constexpr int CPR = D / 8;                    // 16-byte chunks per row
-  constexpr int KRPP = kPfThreads / CPR;        // K rows staged per pass
+  constexpr int KRPP = kShortThreads / CPR;     // K rows staged per pass
   constexpr int KPASS = kPfKTile / KRPP;
   constexpr int VTHREADS = (kPfKTile / 4) * CPR;  // (4-key quad, chunk) pairs
   const int kvh = h / a.group;
-  const int kv_end = a.causal ? min(len, q0 + kPfQTile) : len;
+  const int kv_end = a.causal ? min(len, q0 + kShortQTile) : len;
   const int n_kt = (kv_end + kPfKTile - 1) / kPfKTile;
 
   const int t = threadIdx.x, lane = t & 63;
@@ -140,16 +343,8 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
   const int col = lane & 31, hh = lane >> 5;
   const int qi = q0 + 32 * w + col;  // this lane's query, relative to the sequence
   const int wq0 = q0 + 32 * w;       // the wave's first query
-
-  // Q^T operand: query qi, dims 16 ks + 8 hh .. +7 (rows past the end are 0)
-  u32x4 qv[KS];
-  {
-    const uint8_t* qp =
-        a.q + (s0 + min(qi, len - 1)) * a.q_tok_b + ((int64_t)h * D + 8 * hh) * 2;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qv[ks] = qi < len ? *reinterpret_cast<const u32x4*>(qp + 32 * ks) : u32x4{0, 0, 0, 0};
-  }
+  W st;
+  st.init(a, h, s0, len, qi, hh);
 
   // staging: K row kr + KRPP p, chunk kc; V keys 4 vq .. 4 vq + 3, chunk vc
   const uint8_t* kbase = a.k + s0 * a.k_tok_b + (int64_t)kvh * D * 2;
@@ -194,10 +389,10 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
     }
   };
   auto store_k = [&](int slot) {
-    uint8_t* st = lds + slot * K_BYTES;
+    uint8_t* sk = lds + slot * K_BYTES;
 #pragma unroll
     for (int p = 0; p < KPASS; ++p)
-      *reinterpret_cast<u32x4*>(st + (kr + KRPP * p) * KPITCH + kc * 16) = kreg[p];
+      *reinterpret_cast<u32x4*>(sk + (kr + KRPP * p) * KPITCH + kc * 16) = kreg[p];
   };
   auto store_v = [&](int kt, int slot) {
     if (t >= VTHREADS) return;
@@ -216,95 +411,18 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
           u32x2{pack_hi(x[0][wd], x[1][wd]), pack_hi(x[2][wd], x[3][wd])};
     }
   };
-
-  // S^T of tile kt (K stage kt & 1); the two 32-key blocks alternate so that
-  // neighbouring MFMAs are independent
-  auto qk = [&](int kt, f32x16 (&s)[2]) {
-    const uint8_t* kp = lds + (kt & 1) * K_BYTES + col * KPITCH + 16 * hh;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-        s[sb] = E::mfma(*reinterpret_cast<const u32x4*>(kp + 32 * sb * KPITCH + 32 * ks),
-                        qv[ks], s[sb]);
-  };
-  // -inf where a key is past the end or (causal) after the query; only the
-  // tiles that reach past the wave's first query or the end need it
-  auto mask = [&](int kt, f32x16 (&s)[2]) {
-    const int k0 = kt * kPfKTile;
-    if ((a.causal && k0 + kPfKTile - 1 > wq0) || k0 + kPfKTile > len) {
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kv = k0 + 32 * sb + 8 * (i >> 2) + 4 * hh + (i & 3);
-          const bool ok = kv < len && (!a.causal || kv <= qi);
-          s[sb][i] = ok ? s[sb][i] : -INFINITY;
-        }
-    }
-  };
-
-  f32x16 o[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m = -INFINITY, lsum = 0.f;
-
-  // softmax of a masked S^T tile and O^T += V^T . P^T (V stage kt & 1)
-  auto softmax_pv = [&](int kt, f32x16 (&s)[2]) {
-    float bm = max3(s[0][0], s[0][1], s[0][2]);  // raw-score max (the scale is positive)
-#pragma unroll
-    for (int i = 3; i < 31; i += 2) {
-      const int sb = i >> 4, e = i & 15;
-      bm = max3(bm, s[sb][e], s[(i + 1) >> 4][(i + 1) & 15]);
-    }
-    bm = max3(bm, s[1][15], s[1][15]);  // all 32 of this lane's scores
-    const float pm = __shfl_xor(bm, 32);  // the partner lane's (same query)
-    bm = max3(bm, pm, pm) * a.scale_log2;
-    if (__builtin_amdgcn_ballot_w64(bm > m + kPfRescaleSlack)) {
-      const float mn = fmaxf(m, bm);
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 while m = -inf
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) o[db] *= alpha;
-      m = mn;
-    }
-    const float nms = m == -INFINITY ? 0.f : -m;
-    u32x4 pb[4];  // P^T operands of the four 16-key steps
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int sb = kk >> 1, base = 8 * (kk & 1);
-      uint32_t pw[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p0 =
-            __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][base + 2 * j], a.scale_log2, nms));
-        const float p1 =
-            __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][base + 2 * j + 1], a.scale_log2, nms));
-        lsum += p0 + p1;
-        pw[j] = E::pack(p0, p1);
-      }
-      pb[kk] = u32x4{pw[0], pw[1], pw[2], pw[3]};
-    }
+  auto pv = [&](int kt, const u32x4 (&pb)[4]) {
     const uint8_t* vp = lds + 2 * K_BYTES + (kt & 1) * V_BYTES + col * kVtPitch + 16 * hh;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int db = 0; db < DB; ++db)
-        o[db] = E::mfma(*reinterpret_cast<const u32x4*>(vp + 32 * db * kVtPitch + 32 * kk),
-                        pb[kk], o[db]);
+        st.o[db] = E::mfma(*reinterpret_cast<const u32x4*>(vp + 32 * db * kVtPitch + 32 * kk),
+                           pb[kk], st.o[db]);
   };
 
-  // K and V of tile kt + 1 are loaded while tile kt is computed.  Two
-  // workgroups per CU overlap each other's softmax and matrix work; issuing
-  // the next tile's S^T before the softmax inside the wave (a one-tile
-  // pipeline) measured 1.8x slower, as its second S^T buffer leaves room for
-  // one workgroup per CU only.
+  // K and V of tile kt + 1 are loaded while tile kt is computed; two
+  // workgroups per CU overlap each other's softmax and matrix work.
   load_k(0);
   load_v(0);
   store_k(0);
@@ -316,11 +434,13 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
       load_k(kt + 1);
       load_v(kt + 1);
     }
-    f32x16 sc[2];
     if (!a.causal || kt * kPfKTile <= wq0 + 31) {
-      qk(kt, sc);
-      mask(kt, sc);
-      softmax_pv(kt, sc);
+      f32x16 sc[2];
+      u32x4 pb[4];
+      st.template qk<KPITCH, 0>(lds + (kt & 1) * K_BYTES + col * KPITCH + 16 * hh, sc);
+      st.mask(sc, kt * kPfKTile, wq0, qi, len, a.causal, hh);
+      st.template softmax<false>(sc, pb, a.scale_log2);
+      pv(kt, pb);
     }
     if (more) {
       store_k((kt + 1) & 1);
@@ -328,52 +448,232 @@ __device__ __forceinline__ void attend_tile(const PrefillArgs& a, uint8_t* lds, 
     }
     __syncthreads();
   }
-
-  const float lt = lsum + __shfl_xor(lsum, 32);
-  if (qi < len) {
-    const float inv = 1.f / lt;
-    uint8_t* op = a.out + (s0 + qi) * a.o_tok_b + ((int64_t)h * D + 4 * hh) * 2;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x16& r = o[db];
-        *reinterpret_cast<u32x2*>(op + (32 * db + 8 * g) * 2) =
-            u32x2{E::pack(r[4 * g] * inv, r[4 * g + 1] * inv),
-                  E::pack(r[4 * g + 2] * inv, r[4 * g + 3] * inv)};
-      }
-  }
+  st.store(a, h, s0, len, qi, hh);
 }
 
 template <int DT, int D>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_attention_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kShortThreads, 2) void prefill_short_kernel(PrefillArgs a) {
   constexpr int K_BYTES = kPfKTile * (D * 2 + 16);
   constexpr int V_BYTES = D * kVtPitch;
   // two K stages, then two V^T stages
   __shared__ __align__(16) uint8_t lds[2 * K_BYTES + 2 * V_BYTES];
-  // XCD x's run of units [u0, u1); its s-th job: tile n_qtiles-1 - s / c,
-  // unit u0 + s % c (all uniform over the workgroup)
-  const int x = (int)(blockIdx.x % kXcds), sj = (int)(blockIdx.x / kXcds);
-  const int u0 = (int)((int64_t)a.n_units * x / kXcds);
-  const int c = (int)((int64_t)a.n_units * (x + 1) / kXcds) - u0;
-  if (c == 0 || sj >= a.n_qtiles * c) return;
-  const int tile = a.n_qtiles - 1 - sj / c;
-  const int unit = u0 + sj % c;
-  const int b = unit / a.n_q_heads;
-  const int h = unit % a.n_q_heads;
-  int64_t s0 = a.cu_seqlens[b], s1 = a.cu_seqlens[b + 1];
-  s0 = min(max(s0, (int64_t)0), a.total_tokens);
-  s1 = min(max(s1, s0), a.total_tokens);
-  const int len = (int)min(s1 - s0, (int64_t)a.max_seqlen);
-  const int q0 = tile * kPfQTile;
-  if (q0 >= len) return;  // uniform over the workgroup, before any barrier
-  attend_tile<DT, D>(a, lds, h, s0, len, q0);
+  int h, len, q0;
+  int64_t s0;
+  if (!pick_job(a, kShortQTile, h, s0, len, q0)) return;  // uniform, before any barrier
+  attend_short<DT, D>(a, lds, h, s0, len, q0);
+}
+
+// ----------------------------------------------------------------- long prompts
+// Queries [q0, q0 + 256) of head h of the sequence at token s0 with len
+// tokens, ping-pong between the workgroup's halves.
+template <int DT, int D>
+__device__ __forceinline__ void attend_long(const PrefillArgs& a, uint8_t* lds, int h, int64_t s0,
+                                            int len, int q0) {
+  using E = PfOps<DT>;
+  using W = WaveState<DT, D>;
+  constexpr int KPITCH = D * 2 + 16;            // bytes per K row in LDS
+  constexpr int K_BYTES = kPfKTile * KPITCH;
+  // V rows stay untransposed at 2D + 64 bytes: the transposing reads of four
+  // consecutive keys (64 bytes of each) then hit distinct banks
+  constexpr int VPITCH = D * 2 + 64;
+  constexpr int V_BYTES = kPfKTile * VPITCH;
+  constexpr int DB = W::DB;
+  constexpr int CPR = D / 8;                    // 16-byte chunks of a row's data
+  constexpr int CK = KPITCH / 16, CV = VPITCH / 16;  // chunks per stored row
+  constexpr int NK = (CK + kLongWaves - 1) / kLongWaves;
+  constexpr int NV = (CV + kLongWaves - 1) / kLongWaves;
+  constexpr uint32_t kPad = 0xFFFFFFF0u;        // an offset out of every range
+  const int kvh = h / a.group;
+  const int kv_end = a.causal ? min(len, q0 + kLongQTile) : len;
+  const int n_kt = (kv_end + kPfKTile - 1) / kPfKTile;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the tile tests below branch
+  const int half = w >> 2;           // 0: waves 0-3, 1: waves 4-7 (one phase later)
+  const int col = lane & 31, hh = lane >> 5;
+  const int qi = q0 + 32 * w + col;  // this lane's query, relative to the sequence
+  const int wq0 = q0 + 32 * w;       // the wave's first query
+  // the wave's last key tile: causal waves stop at their last query's tile; a
+  // wave past the end of the sequence attends to nothing (-1)
+  const int jw = wq0 >= len ? -1
+                 : a.causal ? min(n_kt - 1, min(wq0 + 31, len - 1) / kPfKTile)
+                            : n_kt - 1;
+  W st;
+  st.init(a, h, s0, len, qi, hh);
+
+  // Direct HBM -> LDS staging through raw buffer ranges over the sequence's K
+  // and V rows of kv head kvh, ending at the last row's last byte.  Lane l of
+  // a load instruction writes LDS bytes [16 l, 16 l + 16) after the
+  // instruction's base, so instruction i of a tile covers stored chunks
+  // [64 i, 64 i + 64); a row's pad chunks and rows past the sequence end get
+  // an out-of-range offset, for which the hardware writes zeros and reads
+  // nothing (zero V keeps P.V finite; those keys' scores are masked).
+  const __amdgpu_buffer_rsrc_t krs =
+      byte_range(a.k + s0 * a.k_tok_b + (int64_t)kvh * D * 2,
+                 (uint32_t)((int64_t)(len - 1) * a.k_tok_b + D * 2));
+  const __amdgpu_buffer_rsrc_t vrs =
+      byte_range(a.v + s0 * a.v_tok_b + (int64_t)kvh * D * 2,
+                 (uint32_t)((int64_t)(len - 1) * a.v_tok_b + D * 2));
+  const uint32_t k_tok = (uint32_t)a.k_tok_b, v_tok = (uint32_t)a.v_tok_b;
+  // instruction ii of wave w: K instruction w + 8 ii, V instruction
+  // (w + 7) % 8 + 8 ii (the spare ones of a tile go to different waves); the
+  // lane's byte offset within a tile
+  uint32_t koffs[NK], voffs[NV];
+#pragma unroll
+  for (int ii = 0; ii < NK; ++ii) {
+    const int c = (w + kLongWaves * ii) * 64 + lane, row = c / CK, ch = c % CK;
+    koffs[ii] = ch < CPR ? row * k_tok + ch * 16 : kPad;
+  }
+#pragma unroll
+  for (int ii = 0; ii < NV; ++ii) {
+    const int c = (((w + kLongWaves - 1) % kLongWaves) + kLongWaves * ii) * 64 + lane;
+    const int row = c / CV, ch = c % CV;
+    voffs[ii] = ch < CPR ? row * v_tok + ch * 16 : kPad;
+  }
+  auto dma_k = [&](int kt) {
+    const uint32_t t0 = kt * kPfKTile * k_tok;
+#pragma unroll
+    for (int ii = 0; ii < NK; ++ii) {
+      const int i = w + kLongWaves * ii;  // uniform
+      if (i < CK)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            krs, (lds_void*)(lds + (kt & 1) * K_BYTES + i * 1024), 16,
+            koffs[ii] == kPad ? kPad : koffs[ii] + t0, 0, 0, 0);
+    }
+  };
+  auto dma_v = [&](int kt) {
+    const uint32_t t0 = kt * kPfKTile * v_tok;
+#pragma unroll
+    for (int ii = 0; ii < NV; ++ii) {
+      const int i = (w + kLongWaves - 1) % kLongWaves + kLongWaves * ii;  // uniform
+      if (i < CV)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            vrs, (lds_void*)(lds + 2 * K_BYTES + (kt & 1) * V_BYTES + i * 1024), 16,
+            voffs[ii] == kPad ? kPad : voffs[ii] + t0, 0, 0, 0);
+    }
+  };
+  // Transposing V reads (ds_read_b64_tr_b16: in each 16-lane group, result
+  // lane j element k is element j % 4 of source lane 4k + j / 4).  Lane
+  // (group G = lane / 16, s = lane % 16) reads 4 dims 16 (G & 1) + 4 (s % 4)
+  // .. + 3 of key 4 (G >> 1) + s / 4; after the transpose it holds dim
+  // 16 (G & 1) + s of keys 4 (G >> 1) .. + 3 (+ 16 kk, + 8 for elements 4-7,
+  // + 32 db for the dims): the A operand of O^T = V^T . P^T.
+  const int vG = lane >> 4, vs = lane & 15;
+  const int vtr_off = (4 * (vG >> 1) + (vs >> 2)) * VPITCH + (16 * (vG & 1) + 4 * (vs & 3)) * 2;
+  auto pv = [&](int kt, const u32x4 (&pb)[4]) {
+    const uint8_t* vb = lds + 2 * K_BYTES + (kt & 1) * V_BYTES + vtr_off;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vb + 16 * kk * VPITCH + 64 * db)));
+        const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vb + (16 * kk + 8) * VPITCH + 64 * db)));
+        st.o[db] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[kk], st.o[db]);
+      }
+    // two reads per MFMA, four MFMAs ahead
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 4 * DB - 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  };
+  auto qk = [&](int kt, f32x16 (&s)[2]) {
+    st.template qk<KPITCH, 2>(lds + (kt & 1) * K_BYTES + col * KPITCH + 16 * hh, s);
+  };
+  auto softmax = [&](int kt, f32x16 (&s)[2], u32x4 (&pb)[4]) {
+    st.mask(s, kt * kPfKTile, wq0, qi, len, a.causal, hh);
+    st.template softmax<true>(s, pb, a.scale_log2);  // one softmax wave per SIMD at a time
+  };
+  // K_{j+1} and V_j (read from slot 2j + 2 on) are loaded in slot 2j, whose
+  // stages were last read in slot 2j - 1
+  auto stage = [&](int j) {
+    if (j + 1 < n_kt) dma_k(j + 1);
+    if (j < n_kt) dma_v(j);
+  };
+
+  // Slots between workgroup barriers.  Phase p of a wave runs in slot
+  // p + half: even p = 2j is the matrix phase of tile j (S_j, then the P.V of
+  // tile j - 1; p = 2 n_kt only the last P.V), odd p = 2j + 1 its softmax.
+  // Tile j's K is read in slots 2j and 2j + 1, its V in slots 2j + 2 and
+  // 2j + 3.  Each half runs its own loop, so S_j lives within one iteration and
+  // only P and O are carried; both halves pass 2 n_kt + 2 barriers after the
+  // prologue's.  The barriers are plain s_barrier: a slot's LDS reads are
+  // consumed by its own MFMAs before its barrier, and the direct loads issued
+  // at the end of slot 2j are waited for (vmcnt) only before the barrier that
+  // ends slot 2j + 1, so they land while slot 2j + 1 computes.
+#define PF_BARRIER() \
+  do { asm volatile("" ::: "memory"); __builtin_amdgcn_s_barrier(); asm volatile("" ::: "memory"); } while (0)
+#define PF_BARRIER_LOADED()                              \
+  do {                                                   \
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     \
+    __builtin_amdgcn_s_barrier();                        \
+    asm volatile("" ::: "memory");                       \
+  } while (0)
+  u32x4 pb[4];
+  dma_k(0);
+  __syncthreads();  // waits for K_0 and the queries
+  if (half == 0) {
+    for (int j = 0; j < n_kt; ++j) {
+      f32x16 sc[2];  // slot 2j
+      if (j <= jw) qk(j, sc);
+      if (j >= 1 && j - 1 <= jw) pv(j - 1, pb);
+      stage(j);
+      PF_BARRIER();
+      if (j <= jw) softmax(j, sc, pb);  // slot 2j + 1
+      PF_BARRIER_LOADED();
+    }
+    if (n_kt - 1 <= jw) pv(n_kt - 1, pb);  // slot 2 n_kt
+    PF_BARRIER();
+    PF_BARRIER();  // slot 2 n_kt + 1: idle
+  } else {
+    stage(0);  // slot 0: idle
+    PF_BARRIER();
+    for (int j = 0; j < n_kt; ++j) {
+      f32x16 sc[2];  // slot 2j + 1
+      if (j <= jw) qk(j, sc);
+      if (j >= 1 && j - 1 <= jw) pv(j - 1, pb);
+      PF_BARRIER_LOADED();
+      if (j <= jw) softmax(j, sc, pb);  // slot 2j + 2
+      stage(j + 1);
+      PF_BARRIER();
+    }
+    if (n_kt - 1 <= jw) pv(n_kt - 1, pb);  // slot 2 n_kt + 1
+    PF_BARRIER();
+  }
+#undef PF_BARRIER
+#undef PF_BARRIER_LOADED
+  st.store(a, h, s0, len, qi, hh);
 }
 
 template <int DT, int D>
-void launch_prefill(const PrefillArgs& a, uint32_t grid, hipStream_t stream) {
-  hipLaunchKernelGGL((prefill_attention_kernel<DT, D>), dim3(grid), dim3(kPfThreads), 0, stream,
-                     a);
+__global__ __launch_bounds__(kLongThreads) void prefill_long_kernel(PrefillArgs a) {
+  constexpr int K_BYTES = kPfKTile * (D * 2 + 16);
+  constexpr int V_BYTES = kPfKTile * (D * 2 + 64);
+  // two K stages, then two V stages
+  __shared__ __align__(16) uint8_t lds[2 * K_BYTES + 2 * V_BYTES];
+  int h, len, q0;
+  int64_t s0;
+  if (!pick_job(a, kLongQTile, h, s0, len, q0)) return;  // uniform, before any barrier
+  attend_long<DT, D>(a, lds, h, s0, len, q0);
+}
+
+template <int DT, int D>
+void launch_prefill(PrefillArgs a, bool long_prompts, hipStream_t stream) {
+  const int qtile = long_prompts ? kLongQTile : kShortQTile;
+  const int64_t n_qtiles = ((int64_t)a.max_seqlen + qtile - 1) / qtile;
+  a.n_qtiles = (int32_t)n_qtiles;
+  // kXcds runs of at most ceil(n_units / kXcds) units each
+  const uint32_t grid = (uint32_t)(kXcds * n_qtiles * ((a.n_units + kXcds - 1) / kXcds));
+  if (long_prompts)
+    hipLaunchKernelGGL((prefill_long_kernel<DT, D>), dim3(grid), dim3(kLongThreads), 0, stream,
+                       a);
+  else
+    hipLaunchKernelGGL((prefill_short_kernel<DT, D>), dim3(grid), dim3(kShortThreads), 0, stream,
+                       a);
 }
 
 }  // namespace
@@ -407,11 +707,18 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
   if (!aligned16(out) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
       q_token_stride % 8 || k_token_stride % 8 || v_token_stride % 8 || out_token_stride % 8)
     return AEGKV_ERR_MISALIGNED;
-  const int64_t n_qtiles = ((int64_t)max_seqlen + kPfQTile - 1) / kPfQTile;
   const int64_t n_units = (int64_t)n_q_heads * batch;
-  // kXcds runs of at most ceil(n_units / kXcds) units each
+  // the short kernel's grid is the larger: 128-query tiles
+  const int64_t n_qtiles = ((int64_t)max_seqlen + kShortQTile - 1) / kShortQTile;
   const int64_t grid = kXcds * n_qtiles * ((n_units + kXcds - 1) / kXcds);
   if (grid > INT32_MAX || n_units * n_qtiles > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
+  // the long kernel addresses K and V rows by 32-bit byte offsets within a
+  // sequence, up to one key tile past its end
+  const bool long_prompts = max_seqlen > kLongPrompt;
+  if (long_prompts && ((int64_t)max_seqlen + kPfKTile) *
+                              std::max(k_token_stride, v_token_stride) * 2 >
+                          (int64_t)UINT32_MAX)
+    return AEGKV_ERR_UNSUPPORTED;
 
   PrefillArgs a;
   a.q = static_cast<const uint8_t*>(q);
@@ -428,17 +735,16 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
   a.n_q_heads = n_q_heads;
   a.group = n_q_heads / n_kv_heads;
   a.max_seqlen = max_seqlen;
-  a.n_qtiles = (int32_t)n_qtiles;
+  a.n_qtiles = 0;  // set per kernel
   a.n_units = (int32_t)n_units;
   a.causal = causal ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const uint32_t g = (uint32_t)grid;
   if (dtype == AEGKV_DTYPE_BF16) {
-    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_BF16, 64>(a, g, stream);
-    else launch_prefill<AEGKV_DTYPE_BF16, 128>(a, g, stream);
+    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_BF16, 64>(a, long_prompts, stream);
+    else launch_prefill<AEGKV_DTYPE_BF16, 128>(a, long_prompts, stream);
   } else {
-    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_FP16, 64>(a, g, stream);
-    else launch_prefill<AEGKV_DTYPE_FP16, 128>(a, g, stream);
+    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_FP16, 64>(a, long_prompts, stream);
+    else launch_prefill<AEGKV_DTYPE_FP16, 128>(a, long_prompts, stream);
   }
   AEGKV_HIP_TRY(hipGetLastError());
   return AEGKV_OK;

@@ -292,14 +292,16 @@ def varlen_prefill_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
         n = s1 - s0
         if n <= 0:
             continue
-        qb = q[s0:s1].astype(np.float64).reshape(n, Hkv, G, D)
-        kb = k[s0:s1].astype(np.float64)
-        vb = v[s0:s1].astype(np.float64)
-        s = np.einsum("ihgd,jhd->hgij", qb, kb) * scale
+        # [Hkv, G, n, D] queries against [Hkv, 1, n, D] keys and values
+        # (batched matrix products, so long prompts finish in seconds)
+        qb = q[s0:s1].astype(np.float64).reshape(n, Hkv, G, D).transpose(1, 2, 0, 3)
+        kb = k[s0:s1].astype(np.float64).transpose(1, 0, 2)[:, None]
+        vb = v[s0:s1].astype(np.float64).transpose(1, 0, 2)[:, None]
+        s = np.matmul(qb, kb.transpose(0, 1, 3, 2)) * scale
         if causal:
             s = np.where(np.tril(np.ones((n, n), dtype=bool)), s, -np.inf)
         s -= s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=-1, keepdims=True)
-        out[s0:s1] = np.einsum("hgij,jhd->ihgd", p, vb).reshape(n, Hq, D)
+        out[s0:s1] = np.matmul(p, vb).transpose(2, 0, 1, 3).reshape(n, Hq, D)
     return out

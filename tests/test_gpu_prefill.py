@@ -57,6 +57,61 @@ def test_ragged_batch_matches_oracle(Hq, Hkv, D, causal):
     _check(out, q, k, v, cu, scale, causal, torch.bfloat16)
 
 
+LONG_LENS = [1537, 1, 255, 256, 257, 2000, 64, 33]  # longest > 1536: the ping-pong kernel
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(8, 2, 128), (12, 3, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_prompts_match_oracle(Hq, Hkv, D, causal, dtype):
+    """Batches whose longest prompt exceeds 1536 tokens run on the eight-wave
+    ping-pong kernel (direct-to-LDS K/V, transposing V reads); lengths at and
+    around the 64-key and 256-query tile edges, a 1-token prompt."""
+    cu, q, k, v = _packed(LONG_LENS, Hq, Hkv, D, dtype, 31 + D)
+    scale = 1.0 / math.sqrt(D)
+    out = A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), max(LONG_LENS), scale,
+                                     causal)
+    _check(out, q, k, v, cu, scale, causal, dtype)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_and_short_kernels_bit_identical(D, causal, dtype):
+    """The same prompts through both kernels: the exact host bound (1000,
+    the four-wave kernel) and a loose bound of 2048 (the ping-pong kernel).
+    Both accumulate every product in the same order, so the outputs are equal
+    bit for bit; the short run is also checked against the oracle."""
+    lens = [1000, 65, 1, 640, 129, 999]
+    cu, q, k, v = _packed(lens, 8, 2, D, dtype, 77 + D)
+    cu_t = torch.from_numpy(cu).cuda()
+    short = A.varlen_prefill_attention(q, k, v, cu_t, max(lens), 0.09, causal)
+    long = A.varlen_prefill_attention(q, k, v, cu_t, 2048, 0.09, causal)
+    torch.cuda.synchronize()
+    assert torch.equal(short.view(torch.int16), long.view(torch.int16))
+    _check(short, q, k, v, cu, 0.09, causal, dtype)
+
+
+def test_long_prompts_strided_views():
+    """The ping-pong kernel on column slices of a fused QKV projection (token
+    strides differ from the rows) with out a slice of a wider buffer."""
+    Hq, Hkv, D = 28, 4, 128
+    lens = [1800, 90]
+    T = sum(lens)
+    g = torch.Generator(device="cuda").manual_seed(13)
+    qkv = torch.randn((T, (Hq + 2 * Hkv) * D), generator=g, device="cuda").to(torch.bfloat16)
+    q = qkv[:, :Hq * D].view(T, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D)
+    v = qkv[:, (Hq + Hkv) * D:].view(T, Hkv, D)
+    wide = torch.full((T, Hq * D + 64), 7.0, device="cuda", dtype=torch.bfloat16)
+    out = wide[:, :Hq * D].view(T, Hq, D)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), max(lens), 0.088, True,
+                               out=out)
+    _check(out, q, k, v, cu, 0.088, True, torch.bfloat16)
+    assert bool((wide[:, Hq * D:] == 7.0).all())
+
+
 @pytest.mark.parametrize("D", [64, 128])
 def test_fp16(D):
     lens = [200, 7, 129]
@@ -86,7 +141,8 @@ def test_strided_views_of_fused_qkv():
     assert bool((wide[:, Hq * D:] == 7.0).all())
 
 
-def test_empty_sequences_loose_bound_and_nan_padding():
+@pytest.mark.parametrize("bound", [400, 2048])  # the four-wave and the ping-pong kernel
+def test_empty_sequences_loose_bound_and_nan_padding(bound):
     """Zero-length sequences, a host bound above every length, and NaN rows
     after the last sequence (padding tokens): the outputs of real tokens are
     right and padding rows of out are not written."""
@@ -96,7 +152,7 @@ def test_empty_sequences_loose_bound_and_nan_padding():
     for x in (q, k, v):
         x[n:] = float("nan")
     out = torch.full_like(q, 3.0)
-    A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), 400, 0.125, True, out=out)
+    A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), bound, 0.125, True, out=out)
     _check(out, q, k, v, cu, 0.125, True, torch.bfloat16)
     assert bool((out[n:] == 3.0).all())
 
@@ -119,14 +175,22 @@ def test_lengths_clamped_to_host_bound():
            True, torch.bfloat16)
 
 
-def test_deterministic():
-    lens = [300, 77]
+@pytest.mark.parametrize("lens", [[300, 77], [2000, 300, 77, 700]])  # four-wave, ping-pong
+@pytest.mark.parametrize("causal", [True, False])
+def test_deterministic(lens, causal):
+    """Repeated calls give the same bits (the ping-pong kernel's register
+    exchange between the wave halves included), and so does the other kernel
+    on the same prompts (a host bound of 1536 or 2048)."""
     cu, q, k, v = _packed(lens, 28, 4, 128, torch.bfloat16, 12)
     cu_t = torch.from_numpy(cu).cuda()
-    a = A.varlen_prefill_attention(q, k, v, cu_t, 300, 0.088, True)
-    b = A.varlen_prefill_attention(q, k, v, cu_t, 300, 0.088, True)
+    runs = [A.varlen_prefill_attention(q, k, v, cu_t, max(lens), 0.088, causal) for _ in range(5)]
+    other = A.varlen_prefill_attention(q, k, v, cu_t, 1536 if max(lens) > 1536 else 2048, 0.088,
+                                       causal)
     torch.cuda.synchronize()
-    assert torch.equal(a, b)
+    for r in runs[1:]:
+        assert torch.equal(runs[0].view(torch.int16), r.view(torch.int16))
+    if max(lens) <= 1536:  # a bound below the longest prompt clamps it: compare only then
+        assert torch.equal(runs[0].view(torch.int16), other.view(torch.int16))
 
 
 def _torch_reference(q, k, v, cu, scale):
