@@ -821,7 +821,19 @@ def bench_copy_floor(args, timer):
         raise RuntimeError("copy floor: the copy is wrong")
     del src, outs
     torch.cuda.empty_cache()
-    return {"bytes": 2 * FLOOR_BLOCKS * FLOOR_BLOCK_BYTES, "ms": ms}
+    # the launch floor: the same kernel moving (almost) nothing, back to back,
+    # as one workgroup (one 16-byte block) and as a full-chip grid (8192
+    # workgroups, one 16-byte block each)
+    floors = {}
+    for label, n in (("one_workgroup", 1), ("grid_8192_workgroups", 8192)):
+        tiny = torch.ones((n, 16), dtype=torch.uint8, device=dev)
+        tiny_out = torch.empty_like(tiny)
+        ops.copy_blocks(tiny, tiny_out, None, None)
+        torch.cuda.synchronize()
+        floors[label], _ = timer.run(lambda i: ops.copy_blocks(tiny, tiny_out, None, None),
+                                     args.steps)
+        del tiny, tiny_out
+    return {"bytes": 2 * FLOOR_BLOCKS * FLOOR_BLOCK_BYTES, "ms": ms, "launch_floor_ms": floors}
 
 
 # ---------------------------------------------------------------------- CPU baseline
@@ -1151,6 +1163,10 @@ def main(argv=None):
                         "rotated regions",
             "us": round(f["ms"] * 1e3, 2), "bytes": f["bytes"], "GB/s": round(fg, 1),
             "frac_hbm": round(fg / HBM_PEAK_GBS, 4)}
+        ops_out["launch_floor_us"] = {
+            "workload": "the block-copy kernel moving 16-byte blocks back to back: the fixed "
+                        "cost of a launch that moves no data",
+            **{k: round(v * 1e3, 2) for k, v in f["launch_floor_ms"].items()}}
     line["ops"] = ops_out
     if cpu is not None:
         line["cpu_baseline"] = cpu
