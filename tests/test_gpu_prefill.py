@@ -3,9 +3,13 @@ prompt run reached from aegaeon/aegaeon/worker.py:517-523) against the
 oracle's float64 textbook attention, through the C ABI.
 
 Tolerance: the kernel rounds P to 16 bits before P.V, as FlashAttention does,
-and rounds the output to the I/O dtype.  Against float64 the bar is a relative
-L2 error of 4e-3 (bf16) / 1e-3 (fp16) per call, and an elementwise error of at
-most 2^-6 (bf16) / 2^-8 (fp16) of the output's largest magnitude."""
+and rounds the output to the I/O dtype.  The output's own rounding already
+costs ~1.6e-3 relative L2 in bf16 (~2.0e-4 in fp16) against float64, so a flat
+2e-3 bar would leave P's rounding ~0.4e-3.  The bar is therefore the relative
+L2 error of the float64 result rounded to the I/O dtype plus 1e-3 (bf16) /
+1.5e-4 (fp16) for P's rounding (measured excess: at most 0.7e-3 / 0.09e-3),
+and an elementwise error of at most 2^-6 (bf16) / 2^-8 (fp16) of the output's
+largest magnitude."""
 import math
 
 import numpy as np
@@ -18,7 +22,7 @@ from oracle import kv_oracle as ko
 
 pytestmark = pytest.mark.gpu
 
-BARS = {torch.bfloat16: (4e-3, 2.0 ** -6), torch.float16: (1e-3, 2.0 ** -8)}
+BARS = {torch.bfloat16: (1e-3, 2.0 ** -6), torch.float16: (1.5e-4, 2.0 ** -8)}
 
 
 def _packed(lens, Hq, Hkv, D, dtype, seed, extra=0):
@@ -38,10 +42,12 @@ def _check(got, q, k, v, cu, scale, causal, dtype, n_tokens=None):
                                       v[:n].double().cpu().numpy(), cu, scale, causal)
     out = got[:n].double().cpu().numpy()
     assert np.isfinite(out).all()
-    rel, elem = BARS[dtype]
-    err = np.linalg.norm(out - ref) / max(np.linalg.norm(ref), 1e-30)
+    extra, elem = BARS[dtype]
+    nref = max(np.linalg.norm(ref), 1e-30)
+    err = np.linalg.norm(out - ref) / nref
+    rounding = np.linalg.norm(torch.from_numpy(ref).to(dtype).double().numpy() - ref) / nref
     worst = np.abs(out - ref).max() / max(np.abs(ref).max(), 1e-30)
-    assert err <= rel, (err, worst)
+    assert err <= rounding + extra, (err, rounding, worst)
     assert worst <= elem, (err, worst)
     return err
 
@@ -193,40 +199,16 @@ def test_deterministic(lens, causal):
         assert torch.equal(runs[0].view(torch.int16), other.view(torch.int16))
 
 
-def _torch_reference(q, k, v, cu, scale):
-    """float32 causal attention on the GPU, one sequence at a time (operands
-    made contiguous before every product)."""
-    T, Hq, D = q.shape
-    G = Hq // k.size(1)
-    out = torch.zeros((T, Hq, D), dtype=torch.float32, device=q.device)
-    for b in range(len(cu) - 1):
-        s0, s1 = int(cu[b]), int(cu[b + 1])
-        n = s1 - s0
-        qf = q[s0:s1].float().transpose(0, 1).contiguous()
-        kf = k[s0:s1].float().transpose(0, 1).repeat_interleave(G, 0)
-        vf = v[s0:s1].float().transpose(0, 1).repeat_interleave(G, 0).contiguous()
-        s = torch.bmm(qf, kf.transpose(1, 2).contiguous()) * scale
-        s.masked_fill_(torch.ones((n, n), dtype=torch.bool, device=q.device).triu(1), -math.inf)
-        p = torch.softmax(s, dim=-1)
-        out[s0:s1] = torch.bmm(p, vf).transpose(0, 1)
-    return out
-
-
 def test_qwen_prompt_batch_full_size():
     """Qwen2.5-7B prompt run, 4 prompts x 2048 tokens, GQA 28/4, D 128, bf16,
-    against float32 attention computed on the GPU."""
+    against the float64 oracle at full size."""
     lens = [2048] * 4
     cu, q, k, v = _packed(lens, 28, 4, 128, torch.bfloat16, 21)
     scale = 1.0 / math.sqrt(128)
     out = A.flash_attn_varlen_func(q, k, v, torch.from_numpy(cu).cuda(),
                                    torch.from_numpy(cu).cuda(), 2048, 2048, softmax_scale=scale,
                                    causal=True)
-    ref = _torch_reference(q, k, v, cu, scale)
-    torch.cuda.synchronize()
-    err = (out.float() - ref).norm() / ref.norm()
-    worst = (out.float() - ref).abs().max() / ref.abs().max()
-    assert float(err) <= 4e-3, float(err)
-    assert float(worst) <= 2.0 ** -6, float(worst)
+    _check(out, q, k, v, cu, scale, True, torch.bfloat16)
 
 
 def test_wrapper_rejects_unsupported_options():
