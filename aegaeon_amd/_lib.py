@@ -32,7 +32,7 @@ SIGNATURES: Dict[str, tuple] = {
                                           c_void_p, c_uint64, c_void_p]),
     "aegkv_signals_create": (c_int, [c_int64, POINTER(c_void_p), c_void_p]),
     "aegkv_signals_destroy": (c_int, [c_void_p]),
-    "aegkv_signals_open": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "aegkv_signals_open": (c_int, [c_void_p, POINTER(c_void_p), POINTER(c_int64)]),
     "aegkv_signals_close": (c_int, [c_void_p]),
     "aegkv_signal_set": (c_int, [c_void_p, c_uint64, c_void_p]),
     "aegkv_signal_wait": (c_int, [c_void_p, c_uint64, c_uint64, c_void_p, c_void_p]),

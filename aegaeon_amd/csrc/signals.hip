@@ -5,7 +5,9 @@
 //
 // A signal array is a few 64-bit timeline words in device memory that one
 // process allocates and exports with hipIpcGetMemHandle; other processes on the
-// node open it.  A producer stream finishes a move with signal_set (one lane
+// node open it.  The allocation starts with a header word holding the array's
+// word count, so an opening process learns the bounds; the words handed out
+// follow it.  A producer stream finishes a move with signal_set (one lane
 // stores the move's serial with a system-scope release after everything
 // before it in the stream); a consumer stream that must not start before that
 // move runs signal_wait (one lane polls the word with system-scope acquire
@@ -22,6 +24,8 @@
 
 namespace aegkv {
 namespace {
+
+constexpr int64_t kMaxSignalWords = 1 << 20;
 
 __global__ __launch_bounds__(64) void signal_set_kernel(uint64_t* word, uint64_t value) {
   if (threadIdx.x == 0)
@@ -49,10 +53,14 @@ using namespace aegkv;
 extern "C" {
 
 int aegkv_signals_create(int64_t n_words, void** words, void* ipc_handle) {
-  if (n_words <= 0 || !words || !ipc_handle) return AEGKV_ERR_INVALID_ARG;
+  if (n_words <= 0 || n_words > kMaxSignalWords || !words || !ipc_handle)
+    return AEGKV_ERR_INVALID_ARG;
+  const size_t bytes = (size_t)(n_words + 1) * sizeof(uint64_t);
   void* p = nullptr;
-  AEGKV_HIP_TRY(hipMalloc(&p, (size_t)n_words * sizeof(uint64_t)));
-  hipError_t e = hipMemset(p, 0, (size_t)n_words * sizeof(uint64_t));
+  AEGKV_HIP_TRY(hipMalloc(&p, bytes));
+  const uint64_t header = (uint64_t)n_words;
+  hipError_t e = hipMemset(p, 0, bytes);
+  if (e == hipSuccess) e = hipMemcpy(p, &header, sizeof(header), hipMemcpyHostToDevice);
   hipIpcMemHandle_t h;
   if (e == hipSuccess) e = hipIpcGetMemHandle(&h, p);
   if (e != hipSuccess) {
@@ -60,27 +68,36 @@ int aegkv_signals_create(int64_t n_words, void** words, void* ipc_handle) {
     return (int)e;
   }
   std::memcpy(ipc_handle, &h, sizeof(h));
-  *words = p;
+  *words = static_cast<uint64_t*>(p) + 1;
   return AEGKV_OK;
 }
 
 int aegkv_signals_destroy(void* words) {
   if (!words) return AEGKV_ERR_INVALID_ARG;
-  AEGKV_HIP_TRY(hipFree(words));
+  AEGKV_HIP_TRY(hipFree(static_cast<uint64_t*>(words) - 1));
   return AEGKV_OK;
 }
 
-int aegkv_signals_open(const void* ipc_handle, void** words) {
-  if (!ipc_handle || !words) return AEGKV_ERR_INVALID_ARG;
+int aegkv_signals_open(const void* ipc_handle, void** words, int64_t* n_words) {
+  if (!ipc_handle || !words || !n_words) return AEGKV_ERR_INVALID_ARG;
   hipIpcMemHandle_t h;
   std::memcpy(&h, ipc_handle, sizeof(h));
-  AEGKV_HIP_TRY(hipIpcOpenMemHandle(words, h, hipIpcMemLazyEnablePeerAccess));
+  void* p = nullptr;
+  AEGKV_HIP_TRY(hipIpcOpenMemHandle(&p, h, hipIpcMemLazyEnablePeerAccess));
+  uint64_t header = 0;
+  const hipError_t e = hipMemcpy(&header, p, sizeof(header), hipMemcpyDeviceToHost);
+  if (e != hipSuccess || header == 0 || header > (uint64_t)kMaxSignalWords) {
+    (void)hipIpcCloseMemHandle(p);
+    return e != hipSuccess ? (int)e : AEGKV_ERR_INVALID_ARG;
+  }
+  *words = static_cast<uint64_t*>(p) + 1;
+  *n_words = (int64_t)header;
   return AEGKV_OK;
 }
 
 int aegkv_signals_close(void* words) {
   if (!words) return AEGKV_ERR_INVALID_ARG;
-  AEGKV_HIP_TRY(hipIpcCloseMemHandle(words));
+  AEGKV_HIP_TRY(hipIpcCloseMemHandle(static_cast<uint64_t*>(words) - 1));
   return AEGKV_OK;
 }
 

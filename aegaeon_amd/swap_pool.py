@@ -68,7 +68,8 @@ def bounce_buffer(nbytes: int) -> torch.Tensor:
 class SignalArray:
     """Timeline words in device memory that other processes can open: the
     creator's words come from aegkv_signals_create, an opened array from
-    aegkv_signals_open on the creator's 64-byte handle."""
+    aegkv_signals_open on the creator's 64-byte handle (which also gives the
+    word count, so every process checks its word indexes)."""
 
     def __init__(self, n_words: int = 64, device=None):
         self._lib = _lib.load()
@@ -86,16 +87,23 @@ class SignalArray:
         self = cls.__new__(cls)
         self._lib = _lib.load()
         self.device = torch.device(device)
-        self.n_words = 0
-        ptr = ctypes.c_void_p()
+        if len(handle) != 64:
+            raise ValueError("a signal-array handle is 64 bytes")
+        ptr, n = ctypes.c_void_p(), ctypes.c_int64()
         with torch.cuda.device(self.device):
-            _lib.check(self._lib.aegkv_signals_open(bytes(handle), ctypes.byref(ptr)),
-                       "signals_open")
+            _lib.check(self._lib.aegkv_signals_open(bytes(handle), ctypes.byref(ptr),
+                                                    ctypes.byref(n)), "signals_open")
         self.ptr, self.handle, self.owned = ptr.value, bytes(handle), False
+        self.n_words = int(n.value)
         return self
 
     def word(self, i: int) -> int:
-        return self.ptr + 8 * int(i)
+        i = int(i)
+        if not 0 <= i < self.n_words:
+            raise IndexError(f"signal word {i} outside the array's {self.n_words}")
+        if not self.ptr:
+            raise ValueError("the signal array is closed")
+        return self.ptr + 8 * i
 
     def signal(self, stream: torch.cuda.Stream, i: int, value: int) -> None:
         """After ``stream``'s earlier work, word ``i`` = ``value``."""
@@ -106,14 +114,20 @@ class SignalArray:
              timeout_s: float = 120.0) -> None:
         """``stream``'s later work waits until word ``i`` >= ``value`` (or the
         timeout, which sets the int32 device word ``timed_out``)."""
+        if not (timed_out.is_cuda and timed_out.device == stream.device
+                and timed_out.dtype == torch.int32 and timed_out.numel() >= 1):
+            raise ValueError("timed_out must be an int32 tensor on the stream's GPU")
         _lib.check(self._lib.aegkv_signal_wait(self.word(i), int(value),
                                                max(1, int(timeout_s * 1e6)),
                                                timed_out.data_ptr(), stream.cuda_stream),
                    "signal_wait")
 
     def close(self) -> None:
+        """Free (creator) or unmap (opener) the words once every kernel this
+        process enqueued on them has ended (the device is synchronised)."""
         if self.ptr:
             with torch.cuda.device(self.device):
+                torch.cuda.synchronize(self.device)
                 rc = (self._lib.aegkv_signals_destroy if self.owned
                       else self._lib.aegkv_signals_close)(self.ptr)
             self.ptr = 0
@@ -123,6 +137,7 @@ class SignalArray:
 def reduce_event(array: SignalArray, word: int, serial: int) -> EventHandle:
     """utils.py:306-315: the handle of the move that sets ``word`` of this
     process's ``array`` to ``serial``."""
+    array.word(word)  # bounds check
     return (array.device.index, os.getpid(), array.handle, int(word), int(serial))
 
 

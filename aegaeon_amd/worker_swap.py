@@ -105,13 +105,17 @@ class KVSwapWorker:
         the copy, also filed under every request."""
         stream = self.swap_in_stream if is_swap_in else self.swap_out_stream
         new_event = torch.cuda.Event()
-        self._wait_source_events(stream, new_event, request_ids, source_events)
+        self._wait_source_events(stream, request_ids, source_events)
         for e in _events(after):
             self._wait(stream, e, None)
         with torch.cuda.stream(stream):
             ops.swap(source_block_ids, target_block_ids, is_swap_in, self.kv_cache,
                      self.kv_swap, bounce=None if self.bounce is None else self.bounce[is_swap_in])
         new_event.record(stream)
+        # filed only once recorded: a swap that raised leaves every request's
+        # last event as it was
+        for rid in request_ids:
+            self.move_event_table[rid].append(new_event)
         if self.signals is not None:
             word = 1 if is_swap_in else 0
             self._serial[is_swap_in] += 1
@@ -145,8 +149,7 @@ class KVSwapWorker:
             return
         stream.wait_event(e)
 
-    def _wait_source_events(self, stream: torch.cuda.Stream, new_event: torch.cuda.Event,
-                            request_ids: Sequence[int],
+    def _wait_source_events(self, stream: torch.cuda.Stream, request_ids: Sequence[int],
                             source_events: Iterable[EventLike]) -> None:
         """worker.py:772-815: a request with a move in flight is waited on
         before anything else touches its blocks; the request's own last event
@@ -161,7 +164,6 @@ class KVSwapWorker:
                     evs = [self.move_event_table[rid][-1]]
                 for e in evs:
                     self._wait(stream, e, rid)
-            self.move_event_table[rid].append(new_event)
 
     # -- the compute side (worker.py:473-500) -------------------------------------
     def ready_mask(self, request_ids: Sequence[int]) -> List[bool]:

@@ -110,10 +110,12 @@ int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, in
  * recorded after a swap at worker.py:740,765, waited on with
  * cudaStreamWaitEvent at worker.py:772-815); on this runtime hipEventRecord
  * refuses events created with hipEventInterprocess.  A signal array is
- * n_words 64-bit timeline words of device memory (zeroed), created by one
- * process with its 64-byte hipIpcMemHandle_t written to ipc_handle, opened by
- * the others (aegkv_signals_open / _close; the creator frees it with
- * aegkv_signals_destroy).  These four allocate, open or free device memory.
+ * n_words (1 .. 2^20) 64-bit timeline words of device memory (zeroed), created
+ * by one process with its 64-byte hipIpcMemHandle_t written to ipc_handle,
+ * opened by the others (aegkv_signals_open, which also returns n_words, read
+ * from a header word that precedes *words in the allocation; _close; the
+ * creator frees it with aegkv_signals_destroy).  These four allocate, open or
+ * free device memory; *words is word 0 of the array in every process.
  *   aegkv_signal_set: after the stream's earlier work, *word = value
  *     (system-scope release).  One stream writes a word, with growing values.
  *   aegkv_signal_wait: the stream's later work starts only once
@@ -123,7 +125,7 @@ int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, in
  * word must be 8-byte aligned. */
 int aegkv_signals_create(int64_t n_words, void** words, void* ipc_handle);
 int aegkv_signals_destroy(void* words);
-int aegkv_signals_open(const void* ipc_handle, void** words);
+int aegkv_signals_open(const void* ipc_handle, void** words, int64_t* n_words);
 int aegkv_signals_close(void* words);
 int aegkv_signal_set(void* word, uint64_t value, aegkv_stream_t stream);
 int aegkv_signal_wait(const void* word, uint64_t value, uint64_t timeout_us, uint32_t* timed_out,

@@ -54,10 +54,12 @@ def main():
     ev_in = worker.swap_blocks([7], msg["file_ids"], msg["dev_ids"], [handle], True)
     ev_in.synchronize()
     worker.check_timeouts()
+    opened = swap_pool.rebuild_event(handle)
+    n_words = opened[0].n_words if opened else -1
     want = seeded_blocks(msg["seed"], len(msg["dev_ids"]))
     got = cache[torch.tensor(msg["dev_ids"], device=dev)].view(torch.int16).cpu()
-    ok = bool(torch.equal(got, want))
-    detail = "" if ok else f"{int((got != want).sum())} int16 words differ"
+    ok = bool(torch.equal(got, want)) and n_words == 2
+    detail = "" if ok else f"{int((got != want).sum())} int16 words differ, array of {n_words} words"
 
     # this worker's own swap-out, held so that it is still pending when the
     # parent enqueues the swap-in that waits on it

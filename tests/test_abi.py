@@ -260,3 +260,20 @@ def test_fused_append_host_checks(lib):
     g = lib.aegkv_paged_decode_attention_append_planned
     assert g(p, Hq * D, p, Hq * D, None, Hkv * D, p, Hkv * D, p, p, 16 * Hkv * D, 8, p, 1 << 20,
              p, 2, 64, Hq, Hkv, D, 16, 0.1, 0, 8, p, 1 << 20, None) == INVALID
+
+
+def test_signal_arrays_reject_bad_arguments_on_the_host(lib):
+    words, n = ctypes.c_void_p(), ctypes.c_int64()
+    handle = (ctypes.c_char * 64)()
+    assert lib.aegkv_signals_create(0, ctypes.byref(words), handle) == INVALID
+    assert lib.aegkv_signals_create((1 << 20) + 1, ctypes.byref(words), handle) == INVALID
+    assert lib.aegkv_signals_create(4, None, handle) == INVALID
+    assert lib.aegkv_signals_open(None, ctypes.byref(words), ctypes.byref(n)) == INVALID
+    assert lib.aegkv_signals_open(handle, ctypes.byref(words), None) == INVALID
+    assert lib.aegkv_signals_destroy(None) == INVALID
+    assert lib.aegkv_signals_close(None) == INVALID
+    raw, addr = _buf(64, misalign=4)
+    assert lib.aegkv_signal_set(addr, 1, None) == INVALID       # not 8-byte aligned
+    assert lib.aegkv_signal_wait(addr, 1, 10, None, None) == INVALID
+    raw2, addr2 = _buf(64)
+    assert lib.aegkv_signal_wait(addr2, 1, 0, None, None) == INVALID  # zero timeout

@@ -166,3 +166,29 @@ def test_two_processes_share_file_and_move_events(device, shm_path):
         swap_pool.close_opened()
         err.close()
         os.unlink(shm_path + ".child.log")
+
+
+def test_signal_array_checks_words_and_timeout_word(device):
+    """Word indexes outside the array and a timeout word the wait kernel could
+    not write are refused before any launch."""
+    arr = swap_pool.SignalArray(4, device)
+    try:
+        stream = torch.cuda.current_stream(device)
+        with pytest.raises(IndexError):
+            arr.signal(stream, 4, 1)
+        with pytest.raises(IndexError):
+            swap_pool.reduce_event(arr, -1, 1)
+        with pytest.raises(ValueError):
+            arr.wait(stream, 0, 1, torch.zeros(1, dtype=torch.int32))  # host tensor
+        with pytest.raises(ValueError):
+            arr.wait(stream, 0, 1, torch.zeros(1, dtype=torch.int64, device=device))
+        # a word that is already reached: the wait ends at once
+        timed_out = torch.zeros(1, dtype=torch.int32, device=device)
+        arr.signal(stream, 3, 5)
+        arr.wait(stream, 3, 5, timed_out, timeout_s=10.0)
+        torch.cuda.synchronize(device)
+        assert int(timed_out.item()) == 0
+    finally:
+        arr.close()
+    with pytest.raises(ValueError):
+        arr.word(0)
