@@ -652,6 +652,7 @@ def bench_overlap(args, timer):
 
 # ------------------------------------------------------------------------- prefill
 PREFILL_LENS = [2048] * 4   # the reference's profiled prefill shape i2048b4
+PREFILL_LONG = 8192         # one long prompt: the attention kernel's steady state
 
 
 def bench_prefill(args, timer):
@@ -707,9 +708,31 @@ def bench_prefill(args, timer):
     att_ms, _ = timer.run(attend, 2 * L)
     flops = sum(2 * Hq * D * n * (n + 1) for n in lens)
     app_bytes = 2 * T * 2 * Hkv * D * 2 + 8 * T
-    del cache, qkv
+    del cache, qkv, q, k, v, out
     torch.cuda.empty_cache()
-    return {"append_ms": app_ms, "append_bytes": app_bytes, "attn_ms": att_ms, "flops": flops}
+
+    # one long prompt (the kernel's steady state): 8192 tokens, 8 layers of
+    # distinct fused QKV views (600 MB, beyond the last-level cache)
+    n8, L8 = PREFILL_LONG, 8
+    qkv8 = torch.randn((L8, n8, (Hq + 2 * Hkv) * D), generator=gen, device=dev).to(torch.bfloat16)
+    q8 = qkv8[..., :Hq * D].view(L8, n8, Hq, D)
+    k8 = qkv8[..., Hq * D:(Hq + Hkv) * D].view(L8, n8, Hkv, D)
+    v8 = qkv8[..., (Hq + Hkv) * D:].view(L8, n8, Hkv, D)
+    out8 = torch.empty((n8, Hq, D), dtype=torch.bfloat16, device=dev)
+    cu8 = torch.tensor([0, n8], dtype=torch.int32, device=dev)
+
+    def attend_long(i):
+        layer = i % L8
+        A.flash_attn_varlen_func(q8[layer], k8[layer], v8[layer], cu8, cu8, n8, n8,
+                                 softmax_scale=scale, causal=True, out=out8)
+
+    attend_long(0)
+    torch.cuda.synchronize()
+    long_ms, _ = timer.run(attend_long, 2 * L8)
+    del qkv8, q8, k8, v8, out8
+    torch.cuda.empty_cache()
+    return {"append_ms": app_ms, "append_bytes": app_bytes, "attn_ms": att_ms, "flops": flops,
+            "long_ms": long_ms, "long_flops": 2 * Hq * D * n8 * (n8 + 1)}
 
 
 # ------------------------------------------------------------------- block manager
@@ -1136,6 +1159,14 @@ def main(argv=None):
             "kv_write_us_per_layer": round(pf["append_ms"] * 1e3, 2),
             "kv_write_bytes_per_layer": pf["append_bytes"], "kv_write_GB/s": round(ag, 1),
             "kv_write_frac_hbm": round(ag / HBM_PEAK_GBS, 4)}
+        tl = pf["long_flops"] / (pf["long_ms"] * 1e-3) / 1e12
+        ops_out["prefill_qwen_1x8192"] = {
+            "workload": "Qwen2.5-7B prompt run, one 8192-token prompt (the attention kernel's "
+                        "steady state), GQA 28/4, D 128, bf16, causal, 8 layers of distinct q/k/v "
+                        "views of a fused QKV",
+            "attention_us_per_layer": round(pf["long_ms"] * 1e3, 2),
+            "attention_flops_per_layer": pf["long_flops"], "TFLOP/s": round(tl, 1),
+            "frac_mfma_bf16": round(tl / MFMA_BF16_PEAK_TFLOPS, 4)}
     if "bm" in res:
         b = res["bm"]
         ops_out["block_manager"] = {
