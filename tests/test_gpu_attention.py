@@ -652,3 +652,59 @@ def test_flash_attn_with_kvcache_appends(device):
                                     ko.bits_to_float(kb, "bf16"), ko.bits_to_float(vb, "bf16"),
                                     ko.pad_block_tables(tables), ctx + 1, 1 / math.sqrt(64))
     _check(to_bits(out).reshape(4, 8, 64), ref, "bf16")
+
+
+def test_one_long_sequence_among_short_ones(device):
+    """A 131072-token sequence (8192 blocks) beside short ones and an empty
+    one.  The default grid cuts it into a piece per workgroup; 8192
+    workgroups (the most a call takes) cut it into pieces of about one block,
+    which the combine merges over hundreds of load rounds.  For both grids the
+    planned call equals the unplanned one bit for bit and the output is within
+    the float64 oracle's tolerance.  The appending call over the same tables
+    equals the two-launch pattern and leaves the same cache."""
+    Hq, Hkv, D = 28, 4, 128
+    lens = np.asarray([131072, 1, 17, 5000, 0], dtype=np.int64)
+    rng = np.random.default_rng(71)
+    need = [-(-int(x) // 16) for x in lens]
+    N = sum(need) + 8
+    ids = rng.permutation(N)[:sum(need)]
+    tables, o = [], 0
+    for c in need:
+        tables.append([int(x) for x in ids[o:o + c]])
+        o += c
+    padded = ko.pad_block_tables(tables)
+    gen = torch.Generator(device=device).manual_seed(71)
+    storage = torch.empty((N, 1, 2, 16, Hkv, D), dtype=torch.bfloat16, device=device)
+    storage.normal_(generator=gen)
+    view = storage.permute(1, 2, 0, 3, 4, 5)
+    kc, vc = view[0, 0], view[0, 1]
+    q = torch.randn((len(lens), Hq, D), generator=gen, device=device).to(torch.bfloat16)
+    bt = torch.from_numpy(padded).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    ml = int(lens.max())
+    scale = 1.0 / math.sqrt(D)
+    oracle = ko.paged_decode_attention(ko.bits_to_float(to_bits(q), "bf16"),
+                                       ko.bits_to_float(to_bits(kc), "bf16"),
+                                       ko.bits_to_float(to_bits(vc), "bf16"), padded, lens, scale)
+    for nwg in (0, 8192):
+        ref = A.paged_decode_attention(q, kc, vc, bt, sl, scale, ml, n_workgroups=nwg)
+        plan = A.DecodePlan(bt, sl, ml, Hkv, nwg)
+        got = A.paged_decode_attention(q, kc, vc, None, None, scale, ml, n_workgroups=nwg,
+                                       plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), nwg
+        _check(to_bits(got), oracle, "bf16")
+
+    # the same tables with a new token at the end of each non-empty sequence
+    n = 4
+    key = torch.randn((n, Hkv, D), generator=gen, device=device).to(torch.bfloat16)
+    val = torch.randn((n, Hkv, D), generator=gen, device=device).to(torch.bfloat16)
+    slots = torch.from_numpy(ko.slot_mapping(tables[:n], lens[:n] - 1, lens[:n])).to(device)
+    two = storage.clone()
+    view2 = two.permute(1, 2, 0, 3, 4, 5)
+    A.reshape_and_cache_flash(key, val, view2[0, 0], view2[0, 1], slots)
+    ref = A.paged_decode_attention(q[:n], view2[0, 0], view2[0, 1], bt[:n], sl[:n], scale, ml)
+    got = A.paged_decode_attention(q[:n], kc, vc, bt[:n], sl[:n], scale, ml, key=key, value=val)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(storage.view(torch.int16), two.view(torch.int16))

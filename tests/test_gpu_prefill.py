@@ -40,7 +40,10 @@ def _check(got, q, k, v, cu, scale, causal, dtype, n_tokens=None):
     n = int(cu[-1]) if n_tokens is None else n_tokens
     ref = ko.varlen_prefill_attention(q[:n].double().cpu().numpy(), k[:n].double().cpu().numpy(),
                                       v[:n].double().cpu().numpy(), cu, scale, causal)
-    out = got[:n].double().cpu().numpy()
+    return _within_bars(got[:n].double().cpu().numpy(), ref, dtype)
+
+
+def _within_bars(out, ref, dtype):
     assert np.isfinite(out).all()
     extra, elem = BARS[dtype]
     nref = max(np.linalg.norm(ref), 1e-30)
@@ -209,6 +212,44 @@ def test_qwen_prompt_batch_full_size():
                                    torch.from_numpy(cu).cuda(), 2048, 2048, softmax_scale=scale,
                                    causal=True)
     _check(out, q, k, v, cu, scale, True, torch.bfloat16)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_32k_prompt_sampled_rows(causal, dtype):
+    """A 32768-token prompt (128 query tiles of the ping-pong kernel) beside a
+    300-token one, Qwen2.5-7B heads.  The full float64 textbook is out of
+    reach at this length, so sampled query rows are checked, each against the
+    oracle's decode attention of that query over the keys it sees (keys 0..r
+    of its prompt when causal, all of them otherwise), with the prompt's K/V
+    laid out as 16-token blocks: tile edges, the middle and the last rows."""
+    lens = [32768, 300]
+    Hq, Hkv, D = 28, 4, 128
+    cu, q, k, v = _packed(lens, Hq, Hkv, D, dtype, 41)
+    scale = 1.0 / math.sqrt(D)
+    out = A.varlen_prefill_attention(q, k, v, torch.from_numpy(cu).cuda(), max(lens), scale,
+                                     causal)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(41)
+    rows = [(0, r) for r in [0, 1, 63, 64, 255, 256, 257, 1535, 1536, 4095, 16383, 16384,
+                             32766, 32767]]
+    rows += [(0, int(r)) for r in rng.integers(0, lens[0], 6)] + [(1, 0), (1, 17), (1, 299)]
+    T = int(cu[-1])
+    nblk = -(-T // 16)
+    kf = np.zeros((nblk * 16, Hkv, D))
+    vf = np.zeros((nblk * 16, Hkv, D))
+    kf[:T] = k.double().cpu().numpy()
+    vf[:T] = v.double().cpu().numpy()
+    tables, seen, idx = [], [], []
+    for b, r in rows:
+        first = int(cu[b]) // 16  # every prompt starts on a 16-token boundary here
+        tables.append(list(range(first, first + -(-lens[b] // 16))))
+        seen.append(r + 1 if causal else lens[b])
+        idx.append(int(cu[b]) + r)
+    ref = ko.paged_decode_attention(q[idx].double().cpu().numpy(),
+                                    kf.reshape(nblk, 16, Hkv, D), vf.reshape(nblk, 16, Hkv, D),
+                                    ko.pad_block_tables(tables), seen, scale)
+    _within_bars(out[idx].double().cpu().numpy(), ref, dtype)
 
 
 def test_wrapper_rejects_unsupported_options():
