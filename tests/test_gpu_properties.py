@@ -13,6 +13,12 @@ the oracle (hypothesis, derandomized so every run draws the same cases).
   fp16.  The output is within the float64 oracle's bars, and the two kernels
   (a host bound above 1536 tokens selects the ping-pong kernel) agree bit for
   bit.
+* Byte movers: one decode token per sequence appended into every layer of a
+  random pool (EXT reshape_and_cache_flash, per layer through the storage
+  view), padding and out-of-pool slots skipped, then a random layer range
+  de-paged; a random live set compacted by the defrag kernel; all bit-exact.
+* Step inputs (worker.py:596-676): random prefill/decode mixes, equal to the
+  oracle's restatement of the host loops.
 
 The tolerances are the ones the per-op test files state; their checks are
 reused here.
@@ -147,3 +153,142 @@ def test_prefill_random_batches(device, case):
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), other.view(torch.int16))
     prefill_check(out, q, k, v, cu, scale, causal, tdt)
+
+
+# ------------------------------------------------------------------ byte movers
+@st.composite
+def _append_case(draw):
+    L = draw(st.integers(1, 4))
+    Hkv = draw(st.sampled_from([1, 2, 4, 8]))
+    D = draw(st.sampled_from([64, 128, 256]))
+    n = draw(st.integers(1, 12))
+    edge = st.sampled_from([1, 15, 16, 17, 32, 33])
+    lens = draw(st.lists(st.one_of(st.integers(1, 300), edge), min_size=n, max_size=n))
+    # per token: 0 its own slot, 1 vLLM's padding slot -1, 2 a slot past the pool
+    kinds = draw(st.lists(st.sampled_from([0, 0, 0, 1, 2]), min_size=n, max_size=n))
+    extra = draw(st.integers(0, 40))
+    first = draw(st.integers(0, L - 1))
+    count = draw(st.integers(1, L - first))
+    seed = draw(st.integers(0, 2 ** 31 - 1))
+    return L, Hkv, D, lens, kinds, extra, (first, count), seed
+
+
+def _random_bits_on(device, shape, seed):
+    g = torch.Generator(device=device).manual_seed(seed)
+    return torch.randint(-2 ** 15, 2 ** 15, shape, dtype=torch.int16, generator=g,
+                         device=device)
+
+
+@settings(max_examples=40, **_SETTINGS)
+@given(case=_append_case())
+def test_append_then_gather_random_pools(device, case):
+    """One decode token per sequence appended into every layer of a random
+    [N, L, 2, 16, Hkv, D] pool in one launch (padding slots -1 and slots past
+    the pool skipped), then a random layer range de-paged: both bit-exact
+    against the oracle, NaN bit patterns included."""
+    L, Hkv, D, lens, kinds, extra, (first, count), seed = case
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    need = [-(-int(x) // 16) for x in lens]
+    N = sum(need) + extra + 1
+    ids = rng.permutation(N)[:sum(need)]
+    tables, o = [], 0
+    for c in need:
+        tables.append([int(x) for x in ids[o:o + c]])
+        o += c
+    slots = ko.slot_mapping(tables, lens - 1, lens)
+    kinds = np.asarray(kinds)
+    slots[kinds == 1] = -1
+    slots[kinds == 2] = N * 16 + rng.integers(0, 1000, int((kinds == 2).sum()))
+    storage = _random_bits_on(device, (N, L, 2, 16, Hkv, D), seed)
+    key = _random_bits_on(device, (L, len(lens), Hkv, D), seed + 1)
+    val = _random_bits_on(device, (L, len(lens), Hkv, D), seed + 2)
+    ref = storage.cpu().numpy().view(np.uint16).copy()
+    # the oracle writes every slot >= 0; a slot past the pool is skipped like -1
+    ko.append_layers(key.cpu().numpy().view(np.uint16), val.cpu().numpy().view(np.uint16), ref,
+                     np.where(slots >= N * 16, -1, slots))
+    bf = torch.bfloat16
+    cache = storage.view(bf)
+    A.append_kv(key.view(bf), val.view(bf), cache, torch.from_numpy(slots).to(device))
+    torch.cuda.synchronize()
+    assert np.array_equal(storage.cpu().numpy().view(np.uint16), ref)
+
+    bt = torch.from_numpy(ko.pad_block_tables(tables)).to(device)
+    sl = torch.from_numpy(lens.astype(np.int32)).to(device)
+    out_k, out_v = A.gather_tokens(cache, bt, sl, int(lens.sum()), int(lens.max()),
+                                   layers=(first, count))
+    rk, rv = ko.gather_tokens(ref, tables, lens, layers=list(range(first, first + count)))
+    assert np.array_equal(to_bits(out_k), rk)
+    assert np.array_equal(to_bits(out_v), rv)
+
+
+@st.composite
+def _defrag_case(draw):
+    bb = draw(st.sampled_from([16, 4096, 16400, 65536, 131072]))
+    n = draw(st.integers(2, 300))
+    live = draw(st.lists(st.integers(0, n - 1), min_size=0, max_size=n, unique=True))
+    seed = draw(st.integers(0, 2 ** 31 - 1))
+    return bb, n, live, seed
+
+
+@settings(max_examples=30, **_SETTINGS)
+@given(case=_defrag_case())
+def test_defrag_random_pools(device, case):
+    """A random live set of a pool of n blocks compacted into its dense
+    prefix: the move lists equal the oracle's, the moved blocks land bit for
+    bit, every other block keeps its bytes, and the rewritten tables equal the
+    oracle's."""
+    from aegaeon_amd.pool import plan_compaction, remap_tables
+    bb, n, live, seed = case
+    src, dst = plan_compaction(live, list(range(n)))
+    osrc, odst = ko.plan_defrag(live, list(range(n)))
+    assert list(src) == osrc and list(dst) == odst
+    pool = _random_bits_on(device, (n * bb // 2,), seed)
+    ref = pool.cpu().numpy().view(np.uint8).reshape(n, bb).copy()
+    ref[np.asarray(odst, dtype=np.int64)] = ref[np.asarray(osrc, dtype=np.int64)]
+    from aegaeon_amd import ops
+    ops.defrag_blocks(pool.view(torch.uint8), src, dst, block_bytes=bb)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.cpu().numpy().view(np.uint8).reshape(n, bb), ref)
+    rng = np.random.default_rng(seed)
+    order = rng.permutation(len(live)).tolist()
+    tables = [[live[i] for i in order[j::3]] for j in range(3)]
+    assert remap_tables(tables, src, dst) == ko.apply_defrag(tables, osrc, odst)
+
+
+@st.composite
+def _inputs_case(draw):
+    n_prefill = draw(st.integers(0, 6))
+    n_decode = draw(st.integers(0 if n_prefill else 1, 40))
+    edge = st.sampled_from([1, 15, 16, 17, 31, 32, 33])
+    prompt = st.one_of(st.integers(1, 400), edge)
+    ctxs = st.one_of(st.integers(1, 3000), edge)
+    prefills = draw(st.lists(prompt, min_size=n_prefill, max_size=n_prefill))
+    decodes = draw(st.lists(ctxs, min_size=n_decode, max_size=n_decode))
+    spare = draw(st.lists(st.integers(0, 2), min_size=n_prefill + n_decode,
+                          max_size=n_prefill + n_decode))
+    seed = draw(st.integers(0, 2 ** 31 - 1))
+    return prefills, decodes, spare, seed
+
+
+@settings(max_examples=40, **_SETTINGS)
+@given(case=_inputs_case())
+def test_prepare_inputs_random_batches(device, case):
+    """Random prefill/decode mixes with tables drawn from a permutation of
+    the pool (some holding spare pre-allocated blocks): every output of the
+    device-side preparation equals the oracle's restatement of the worker's
+    host loops, values and dtypes."""
+    from aegaeon_amd import inputs as I
+    from tests.test_gpu_inputs import _compare
+    prefills, decodes, spare, seed = case
+    rng = np.random.default_rng(seed)
+    perm = iter(rng.permutation(1 << 16).tolist())
+    reqs, tables = [], []
+    for i, n in enumerate(prefills):
+        reqs.append((i, rng.integers(0, 32000, n).tolist(), n, 0))
+        tables.append([next(perm) for _ in range(-(-n // 16) + spare[i])])
+    for j, ctx in enumerate(decodes):
+        i = len(prefills) + j
+        reqs.append((i, [int(rng.integers(0, 32000))], ctx + 1, ctx))
+        tables.append([next(perm) for _ in range(-(-(ctx + 1) // 16) + spare[i])])
+    _compare(I.prepare_model_inputs(reqs, tables, device), ko.prepare_model_inputs(reqs, tables))
