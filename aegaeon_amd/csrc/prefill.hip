@@ -52,7 +52,10 @@
 // contiguous runs, one per XCD: the hardware deals workgroup i to XCD
 // i % kXcds, and workgroup i = s * kXcds + x takes the s-th job of XCD x's
 // run.  Every query tile of a unit then runs on one XCD, whose L2 keeps that
-// sequence's K and V for all of them.  Within an XCD the jobs run with the
+// sequence's K and V for all of them.  When the units do not divide evenly
+// over the XCDs and each CU has several tiles to run, a unit's tiles are
+// dealt as S interleaved slices instead (slices_per_unit), so every XCD
+// holds the same number of slices.  Within an XCD the jobs run with the
 // query tile slowest, in decreasing order, so the most expensive tiles (the
 // last of each sequence) are dispatched first.  (A persistent grid dealing the
 // same jobs in snake order measured 5% slower on 4 x 2048 tokens and 60%
@@ -144,6 +147,7 @@ struct PrefillArgs {
   int64_t total_tokens;
   int32_t batch, n_q_heads, group, max_seqlen, n_qtiles, causal;
   int32_t n_units;                             // batch * n_q_heads
+  int32_t slices;                              // interleaved tile slices per unit
   float scale_log2;                            // softmax scale * log2(e), > 0
 };
 
@@ -294,17 +298,22 @@ struct WaveState {
 };
 
 // Uniform job of workgroup blockIdx.x for query tiles of qtile queries:
-// returns false when the tile is empty.
+// returns false when the tile is empty.  Slice v = unit * S + r holds the
+// unit's tiles r, r + S, ...; XCD x's run is slices [v0, v0 + c), and its
+// s-th job is the (s / c)-th largest tile of slice v0 + s % c.
 __device__ __forceinline__ bool pick_job(const PrefillArgs& a, int qtile, int& h, int64_t& s0,
                                          int& len, int& q0) {
-  // XCD x's run of units [u0, u0 + c); its s-th job: tile n_qtiles-1 - s / c,
-  // unit u0 + s % c
   const int x = (int)(blockIdx.x % kXcds), sj = (int)(blockIdx.x / kXcds);
-  const int u0 = (int)((int64_t)a.n_units * x / kXcds);
-  const int c = (int)((int64_t)a.n_units * (x + 1) / kXcds) - u0;
-  if (c == 0 || sj >= a.n_qtiles * c) return false;
-  const int tile = a.n_qtiles - 1 - sj / c;
-  const int unit = u0 + sj % c;
+  const int S = a.slices;
+  const int64_t n_sl = (int64_t)a.n_units * S;
+  const int v0 = (int)(n_sl * x / kXcds);
+  const int c = (int)(n_sl * (x + 1) / kXcds) - v0;
+  if (c == 0) return false;
+  const int k = sj / c, v = v0 + sj % c;
+  const int unit = v / S, r = v - unit * S;
+  const int m = (a.n_qtiles - r + S - 1) / S;  // tiles in slice r
+  if (k >= m) return false;
+  const int tile = r + S * (m - 1 - k);
   const int b = unit / a.n_q_heads;
   h = unit % a.n_q_heads;
   int64_t s1 = a.cu_seqlens[b + 1];
@@ -661,13 +670,36 @@ __global__ __launch_bounds__(kLongThreads) void prefill_long_kernel(PrefillArgs 
   attend_long<DT, D>(a, lds, h, s0, len, q0);
 }
 
+// Tile slices per unit.  With n_units not a multiple of kXcds, whole units
+// leave some XCDs a unit more than others (1 x 8192 tokens of 28 heads: four
+// XCDs hold 4 units, four hold 3, and the latter idle an eighth of the
+// time).  S interleaved slices per unit, the smallest S with S * n_units a
+// multiple of kXcds, even that out.  That pays only when the heaviest XCD's
+// CUs take at least three tiles each: with fewer, its largest tiles set the
+// end whatever the split, and the split unit's K/V fills two XCDs' L2.
+// (Measured, same process: 1 x 8192 505.9 -> 481.8 us, 1 x 16384 2099 ->
+// 1940 us; 1 x 4096, at two tiles per CU, 140.0 -> 145.8 us without the
+// threshold.)
+int slices_per_unit(int64_t n_units, int64_t n_qtiles, int cus_per_xcd) {
+  int64_t g = kXcds;
+  for (int64_t u = n_units % kXcds; u != 0;) {
+    const int64_t t = g % u;
+    g = u;
+    u = t;
+  }
+  const int64_t S = std::min<int64_t>(kXcds / g, n_qtiles);
+  if (S <= 1 || (n_units + kXcds - 1) / kXcds * n_qtiles < 3 * (int64_t)cus_per_xcd) return 1;
+  return (int)S;
+}
+
+// kXcds runs of at most ceil(S * n_units / kXcds) slices of at most
+// ceil(n_qtiles / S) tiles
+int64_t grid_size(int64_t n_units, int64_t n_qtiles, int S) {
+  return kXcds * ((n_qtiles + S - 1) / S) * ((S * n_units + kXcds - 1) / kXcds);
+}
+
 template <int DT, int D>
-void launch_prefill(PrefillArgs a, bool long_prompts, hipStream_t stream) {
-  const int qtile = long_prompts ? kLongQTile : kShortQTile;
-  const int64_t n_qtiles = ((int64_t)a.max_seqlen + qtile - 1) / qtile;
-  a.n_qtiles = (int32_t)n_qtiles;
-  // kXcds runs of at most ceil(n_units / kXcds) units each
-  const uint32_t grid = (uint32_t)(kXcds * n_qtiles * ((a.n_units + kXcds - 1) / kXcds));
+void launch_prefill(const PrefillArgs& a, bool long_prompts, uint32_t grid, hipStream_t stream) {
   if (long_prompts)
     hipLaunchKernelGGL((prefill_long_kernel<DT, D>), dim3(grid), dim3(kLongThreads), 0, stream,
                        a);
@@ -708,13 +740,16 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
       q_token_stride % 8 || k_token_stride % 8 || v_token_stride % 8 || out_token_stride % 8)
     return AEGKV_ERR_MISALIGNED;
   const int64_t n_units = (int64_t)n_q_heads * batch;
-  // the short kernel's grid is the larger: 128-query tiles
-  const int64_t n_qtiles = ((int64_t)max_seqlen + kShortQTile - 1) / kShortQTile;
-  const int64_t grid = kXcds * n_qtiles * ((n_units + kXcds - 1) / kXcds);
-  if (grid > INT32_MAX || n_units * n_qtiles > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
+  const bool long_prompts = max_seqlen > kLongPrompt;
+  const int qtile = long_prompts ? kLongQTile : kShortQTile;
+  const int64_t n_qtiles = ((int64_t)max_seqlen + qtile - 1) / qtile;
+  DeviceState* ds = nullptr;
+  if (int rc = current_device_state(&ds)) return rc;
+  const int slices = slices_per_unit(n_units, n_qtiles, std::max(1, ds->num_cu / kXcds));
+  const int64_t grid = grid_size(n_units, n_qtiles, slices);
+  if (grid > INT32_MAX || kXcds * n_units * n_qtiles > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
   // the long kernel addresses K and V rows by 32-bit byte offsets within a
   // sequence, up to one key tile past its end
-  const bool long_prompts = max_seqlen > kLongPrompt;
   if (long_prompts && ((int64_t)max_seqlen + kPfKTile) *
                               std::max(k_token_stride, v_token_stride) * 2 >
                           (int64_t)UINT32_MAX)
@@ -735,16 +770,18 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
   a.n_q_heads = n_q_heads;
   a.group = n_q_heads / n_kv_heads;
   a.max_seqlen = max_seqlen;
-  a.n_qtiles = 0;  // set per kernel
+  a.n_qtiles = (int32_t)n_qtiles;
   a.n_units = (int32_t)n_units;
+  a.slices = slices;
   a.causal = causal ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
+  const uint32_t g32 = (uint32_t)grid;
   if (dtype == AEGKV_DTYPE_BF16) {
-    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_BF16, 64>(a, long_prompts, stream);
-    else launch_prefill<AEGKV_DTYPE_BF16, 128>(a, long_prompts, stream);
+    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_BF16, 64>(a, long_prompts, g32, stream);
+    else launch_prefill<AEGKV_DTYPE_BF16, 128>(a, long_prompts, g32, stream);
   } else {
-    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_FP16, 64>(a, long_prompts, stream);
-    else launch_prefill<AEGKV_DTYPE_FP16, 128>(a, long_prompts, stream);
+    if (head_dim == 64) launch_prefill<AEGKV_DTYPE_FP16, 64>(a, long_prompts, g32, stream);
+    else launch_prefill<AEGKV_DTYPE_FP16, 128>(a, long_prompts, g32, stream);
   }
   AEGKV_HIP_TRY(hipGetLastError());
   return AEGKV_OK;
