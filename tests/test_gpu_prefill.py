@@ -214,6 +214,24 @@ def test_qwen_prompt_batch_full_size():
     _check(out, q, k, v, cu, scale, True, torch.bfloat16)
 
 
+def test_units_split_into_slices_over_xcds():
+    """92 (prompt, head) units of up to 1536 tokens on the four-wave kernel:
+    92 is not a multiple of the eight XCDs and each CU has several tiles, so
+    every unit's tiles are dealt as two interleaved slices.  The output
+    matches the oracle, and equals the ping-pong kernel's (a loose bound,
+    whole units per XCD) bit for bit."""
+    rng = np.random.default_rng(23)
+    lens = rng.integers(1100, 1537, 23).tolist()
+    lens[5] = 1536
+    cu, q, k, v = _packed(lens, 4, 1, 64, torch.bfloat16, 23)
+    cu_t = torch.from_numpy(cu).cuda()
+    out = A.varlen_prefill_attention(q, k, v, cu_t, 1536, 0.125, True)
+    other = A.varlen_prefill_attention(q, k, v, cu_t, 1537, 0.125, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), other.view(torch.int16))
+    _check(out, q, k, v, cu, 0.125, True, torch.bfloat16)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_32k_prompt_sampled_rows(causal, dtype):
