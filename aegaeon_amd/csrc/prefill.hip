@@ -743,17 +743,18 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
   const bool long_prompts = max_seqlen > kLongPrompt;
   const int qtile = long_prompts ? kLongQTile : kShortQTile;
   const int64_t n_qtiles = ((int64_t)max_seqlen + qtile - 1) / qtile;
-  DeviceState* ds = nullptr;
-  if (int rc = current_device_state(&ds)) return rc;
-  const int slices = slices_per_unit(n_units, n_qtiles, std::max(1, ds->num_cu / kXcds));
-  const int64_t grid = grid_size(n_units, n_qtiles, slices);
-  if (grid > INT32_MAX || kXcds * n_units * n_qtiles > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
+  if (kXcds * n_units * n_qtiles > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
   // the long kernel addresses K and V rows by 32-bit byte offsets within a
   // sequence, up to one key tile past its end
   if (long_prompts && ((int64_t)max_seqlen + kPfKTile) *
                               std::max(k_token_stride, v_token_stride) * 2 >
                           (int64_t)UINT32_MAX)
     return AEGKV_ERR_UNSUPPORTED;
+  DeviceState* ds = nullptr;
+  if (int rc = current_device_state(&ds)) return rc;
+  const int slices = slices_per_unit(n_units, n_qtiles, std::max(1, ds->num_cu / kXcds));
+  const int64_t grid = grid_size(n_units, n_qtiles, slices);
+  if (grid > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
 
   PrefillArgs a;
   a.q = static_cast<const uint8_t*>(q);
