@@ -120,13 +120,16 @@ struct PfOps<AEGKV_DTYPE_FP16> {
   }
 };
 
-// max(a, b, c) in one instruction.  (fmaxf on values the compiler cannot
-// prove canonical, such as MFMA results, costs a v_max_f32 x, x per operand
-// first; the scores here are never signalling NaNs.)
+// max(a, b, c) through the compiler's own max, never inline asm.  The
+// scores are MFMA results, and a VALU read of an MFMA result needs wait states
+// that only the compiler's hazard tracking inserts: it does not see the
+// operands of an inline-asm v_max3_f32.  That form read unfinished scores on
+// unmasked key tiles whenever the matrix core ran late, which showed as
+// run-to-run output differences (one ulp, in ~7% of rows) once the four-wave
+// kernel's workgroups were dealt to CUs in another order.  The compiler's max
+// costs a few canonicalising v_max_f32 (0-3% per call).
 __device__ __forceinline__ float max3(float a, float b, float c) {
-  float r;
-  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+  return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
 }
 
 // {lo16(a), lo16(b)} and {hi16(a), hi16(b)} (v_perm_b32: src1 = bytes 0-3)
@@ -148,6 +151,7 @@ struct PrefillArgs {
   int32_t batch, n_q_heads, group, max_seqlen, n_qtiles, causal;
   int32_t n_units;                             // batch * n_q_heads
   int32_t slices;                              // interleaved tile slices per unit
+  int32_t interleave;                          // slices dealt round-robin over the XCDs
   float scale_log2;                            // softmax scale * log2(e), > 0
 };
 
@@ -299,17 +303,26 @@ struct WaveState {
 
 // Uniform job of workgroup blockIdx.x for query tiles of qtile queries:
 // returns false when the tile is empty.  Slice v = unit * S + r holds the
-// unit's tiles r, r + S, ...; XCD x's run is slices [v0, v0 + c), and its
-// s-th job is the (s / c)-th largest tile of slice v0 + s % c.
+// unit's tiles r, r + S, ...; XCD x holds c slices, the run [v0, v0 + c) or,
+// interleaved, slices x, x + kXcds, ...; its s-th job is the (s / c)-th
+// largest tile of its (s % c)-th slice.
 __device__ __forceinline__ bool pick_job(const PrefillArgs& a, int qtile, int& h, int64_t& s0,
                                          int& len, int& q0) {
   const int x = (int)(blockIdx.x % kXcds), sj = (int)(blockIdx.x / kXcds);
   const int S = a.slices;
   const int64_t n_sl = (int64_t)a.n_units * S;
-  const int v0 = (int)(n_sl * x / kXcds);
-  const int c = (int)(n_sl * (x + 1) / kXcds) - v0;
-  if (c == 0) return false;
-  const int k = sj / c, v = v0 + sj % c;
+  int c, v;
+  if (a.interleave) {
+    c = (int)((n_sl - x + kXcds - 1) / kXcds);
+    if (c <= 0) return false;
+    v = x + kXcds * (sj % c);
+  } else {
+    const int v0 = (int)(n_sl * x / kXcds);
+    c = (int)(n_sl * (x + 1) / kXcds) - v0;
+    if (c == 0) return false;
+    v = v0 + sj % c;
+  }
+  const int k = sj / c;
   const int unit = v / S, r = v - unit * S;
   const int m = (a.n_qtiles - r + S - 1) / S;  // tiles in slice r
   if (k >= m) return false;
@@ -774,6 +787,14 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
   a.n_qtiles = (int32_t)n_qtiles;
   a.n_units = (int32_t)n_units;
   a.slices = slices;
+  // Prompts of different lengths: contiguous runs would give each XCD whole
+  // prompts (8 prompts of 28 heads: one per XCD, the longest setting the
+  // end), so the units are dealt round-robin instead.  That spreads one kv
+  // head's query heads over several L2s, which costs uniform batches 1-4%,
+  // so it is kept for batches the host bound shows to be ragged (fewer
+  // tokens than 90% of batch x max_seqlen).  Same process, 8 prompts of
+  // 77-2048 tokens: 281.7 -> 149.6 us.
+  a.interleave = total_tokens * 10 < (int64_t)batch * max_seqlen * 9 ? 1 : 0;
   a.causal = causal ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
   const uint32_t g32 = (uint32_t)grid;
