@@ -653,6 +653,7 @@ def bench_overlap(args, timer):
 # ------------------------------------------------------------------------- prefill
 PREFILL_LENS = [2048] * 4   # the reference's profiled prefill shape i2048b4
 PREFILL_LONG = 8192         # one long prompt: the attention kernel's steady state
+PREFILL_RAGGED = [1700, 300, 2048, 77, 1024, 640, 129, 2000]  # a mixed prompt batch
 
 
 def bench_prefill(args, timer):
@@ -731,8 +732,30 @@ def bench_prefill(args, timer):
     long_ms, _ = timer.run(attend_long, 2 * L8)
     del qkv8, q8, k8, v8, out8
     torch.cuda.empty_cache()
+
+    # a ragged batch of 8 prompts (77 to 2048 tokens), 8 layers of distinct views
+    rl = PREFILL_RAGGED
+    Tr = sum(rl)
+    qkvr = torch.randn((L8, Tr, (Hq + 2 * Hkv) * D), generator=gen, device=dev).to(torch.bfloat16)
+    qr = qkvr[..., :Hq * D].view(L8, Tr, Hq, D)
+    kr = qkvr[..., Hq * D:(Hq + Hkv) * D].view(L8, Tr, Hkv, D)
+    vr = qkvr[..., (Hq + Hkv) * D:].view(L8, Tr, Hkv, D)
+    outr = torch.empty((Tr, Hq, D), dtype=torch.bfloat16, device=dev)
+    cur = torch.tensor(np.concatenate([[0], np.cumsum(rl)]), dtype=torch.int32, device=dev)
+
+    def attend_ragged(i):
+        layer = i % L8
+        A.flash_attn_varlen_func(qr[layer], kr[layer], vr[layer], cur, cur, max(rl), max(rl),
+                                 softmax_scale=scale, causal=True, out=outr)
+
+    attend_ragged(0)
+    torch.cuda.synchronize()
+    ragged_ms, _ = timer.run(attend_ragged, 4 * L8)
+    del qkvr, qr, kr, vr, outr
+    torch.cuda.empty_cache()
     return {"append_ms": app_ms, "append_bytes": app_bytes, "attn_ms": att_ms, "flops": flops,
-            "long_ms": long_ms, "long_flops": 2 * Hq * D * n8 * (n8 + 1)}
+            "long_ms": long_ms, "long_flops": 2 * Hq * D * n8 * (n8 + 1),
+            "ragged_ms": ragged_ms, "ragged_flops": sum(2 * Hq * D * n * (n + 1) for n in rl)}
 
 
 # ------------------------------------------------------------------- block manager
@@ -1167,6 +1190,14 @@ def main(argv=None):
             "attention_us_per_layer": round(pf["long_ms"] * 1e3, 2),
             "attention_flops_per_layer": pf["long_flops"], "TFLOP/s": round(tl, 1),
             "frac_mfma_bf16": round(tl / MFMA_BF16_PEAK_TFLOPS, 4)}
+        tr = pf["ragged_flops"] / (pf["ragged_ms"] * 1e-3) / 1e12
+        ops_out["prefill_qwen_ragged8"] = {
+            "workload": "Qwen2.5-7B prompt run, 8 prompts of %s tokens, GQA 28/4, D 128, bf16, "
+                        "causal, 8 layers of distinct q/k/v views of a fused QKV"
+                        % "/".join(str(n) for n in PREFILL_RAGGED),
+            "attention_us_per_layer": round(pf["ragged_ms"] * 1e3, 2),
+            "attention_flops_per_layer": pf["ragged_flops"], "TFLOP/s": round(tr, 1),
+            "frac_mfma_bf16": round(tr / MFMA_BF16_PEAK_TFLOPS, 4)}
     if "bm" in res:
         b = res["bm"]
         ops_out["block_manager"] = {
