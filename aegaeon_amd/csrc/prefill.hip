@@ -55,7 +55,9 @@
 // sequence's K and V for all of them.  When the units do not divide evenly
 // over the XCDs and each CU has several tiles to run, a unit's tiles are
 // dealt as S interleaved slices instead (slices_per_unit), so every XCD
-// holds the same number of slices.  Within an XCD the jobs run with the
+// holds the same number of slices.  A ragged batch (by the host bound) deals
+// its units round-robin over the XCDs, so no XCD holds only the longest
+// prompts.  Within an XCD the jobs run with the
 // query tile slowest, in decreasing order, so the most expensive tiles (the
 // last of each sequence) are dispatched first.  (A persistent grid dealing the
 // same jobs in snake order measured 5% slower on 4 x 2048 tokens and 60%
