@@ -36,6 +36,7 @@ SIGNATURES: Dict[str, tuple] = {
     "aegkv_signals_close": (c_int, [c_void_p]),
     "aegkv_signal_set": (c_int, [c_void_p, c_uint64, c_void_p]),
     "aegkv_signal_wait": (c_int, [c_void_p, c_uint64, c_uint64, c_void_p, c_void_p]),
+    "aegkv_signal_read": (c_int, [c_void_p, POINTER(c_uint64), c_void_p]),
     "aegkv_copy_blocks": (c_int, [c_void_p, c_uint64, c_void_p, c_uint64, _i64p, _i64p, c_int64,
                                   c_uint64, c_void_p]),
     "aegkv_pack_blocks": (c_int, [c_void_p, c_uint64, _i64p, c_int64, c_void_p, c_uint64,
@@ -108,6 +109,11 @@ SIGNATURES: Dict[str, tuple] = {
     "aegkv_bm_move_ids": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
                                   _i64p]),
     "aegkv_bm_complete_moves": (c_int, [c_void_p, c_int32, c_int32, c_int64]),
+    "aegkv_bm_pending": (c_int, [c_void_p, _i64p, _i32p, _i32p, _i64p]),
+    "aegkv_bm_resume": (c_int, [c_void_p, c_int64, _i64p, _i64p, _i32p, _i32p]),
+    "aegkv_bm_cancel": (c_int, [c_void_p, c_int64]),
+    "aegkv_bm_complete_move": (c_int, [c_void_p, c_int32, c_int32, c_int64]),
+    "aegkv_bm_reclaim_slabs": (c_int, [c_void_p]),
     "aegkv_bm_table": (c_int, [c_void_p, c_int64, _i32p, _i32p, _i64p, c_void_p, c_int64]),
     "aegkv_bm_flat_tables": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64]),
     "aegkv_bm_stats": (c_int, [c_void_p, c_int32, c_int32, _i64p, _i64p, _i64p, _i64p]),

@@ -15,14 +15,25 @@
 //     runs short, the pending moves of that space are completed — after the
 //     caller's wait callback confirms their copies finished — and their source
 //     blocks reclaimed, as _reclaim_gpu/cpu_move_blocks do (:360-472).
-// Asynchrony (Ray RPC, CUDA/HIP events) stays with the caller: the callback
-// is where the caller waits for the copies of the moves it is asked about.
+// Asynchrony (Ray RPC, CUDA/HIP events) stays with the caller.  Where the
+// reference awaits the pending moves of a space before reclaiming their
+// source blocks (_get_free_blocks -> _reclaim_*_move_blocks, :498-582,
+// :410-472), a call here suspends instead: it keeps what it has done so far
+// (the requests a move has already assigned keep their new tables, as in the
+// reference), returns AEGKV_RECLAIM_PENDING and names the space and the last
+// pending serial; the caller awaits those moves, reclaims them
+// (aegkv_bm_complete_move / aegkv_bm_reclaim_slabs) and resumes the call, which
+// continues at the allocation that ran short.  Between suspension and resume
+// other calls may run, as other coroutines do in the reference's event loop.
+// A caller that can block may instead install a wait callback, called at the
+// same point; the library then reclaims and continues in the same call.
 #include <algorithm>
 #include <cstdint>
 #include <deque>
 #include <map>
 #include <new>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/aegkv.h"
@@ -52,6 +63,24 @@ struct Table {
 
 bool is_gpu(int32_t loc) { return loc >= 0; }
 
+// A suspended allocate_blocks_batched or move_requests.
+struct PendingOp {
+  bool is_move = false;
+  int32_t loc = 0, shape = -1;  // the space whose pending moves it waits for
+  int64_t serial = -1;          // ... up to this serial
+  // allocate: blocks per request, taken in one batch after the reclaim
+  int32_t engine = 0;
+  std::vector<int64_t> ids, counts;  // the call's requests (both kinds)
+  int64_t total = 0;
+  std::vector<char> had;  // the request had a table when the call began
+  // move: the call's requests, where it stopped, and what it has moved
+  int32_t target = 0, source = 0;
+  size_t next = 0;
+  std::vector<int64_t> src, dst, moved, sizes;
+  int32_t mshape = -1;    // the blocks' shape
+  bool reclaimed = false; // resumed: the next allocation does not suspend again
+};
+
 }  // namespace
 
 struct aegkv_block_manager {
@@ -70,6 +99,10 @@ struct aegkv_block_manager {
   void* wait_ctx = nullptr;
   // last move_requests result
   std::vector<int64_t> last_src, last_dst, last_reqs;
+  // suspended calls, and the requests their moves hold
+  std::map<int64_t, PendingOp> ops;
+  int64_t next_op = 1, last_op = 0;
+  std::unordered_set<int64_t> busy;
 };
 
 namespace {
@@ -135,27 +168,52 @@ void reclaim_cpu_slabs(aegkv_block_manager* bm) {
   }
 }
 
-// Complete every pending move from GPU engine `loc` (or from the CPU pool for
-// `shape`) issued up to now, once the caller confirms their copies are done.
-int reclaim_moves(aegkv_block_manager* bm, int32_t loc, int32_t shape) {
-  std::deque<MoveEvent>& q = is_gpu(loc) ? bm->gpu[loc].moves : bm->cpu_moves[shape];
-  if (q.empty()) return AEGKV_OK;
-  const int64_t target = q.back().serial;
-  if (!bm->wait) return AEGKV_ERR_NO_SPACE;
-  if (bm->wait(bm->wait_ctx, loc, shape, target) != 0) return AEGKV_ERR_NO_SPACE;
-  while (!q.empty() && q.front().serial <= target) {
-    MoveEvent ev = std::move(q.front());
-    q.pop_front();
-    if (is_gpu(loc)) reclaim_gpu_once(bm->gpu[loc], ev);
-    else reclaim_cpu_once(bm, ev);
-  }
-  if (!is_gpu(loc)) reclaim_cpu_slabs(bm);
-  return AEGKV_OK;
+std::deque<MoveEvent>& move_queue(aegkv_block_manager* bm, int32_t loc, int32_t shape) {
+  return is_gpu(loc) ? bm->gpu[loc].moves : bm->cpu_moves[shape];
 }
 
-// _get_free_blocks (block_manager.py:498-582).
+// Where an allocation stopped: the space that ran short and its last pending
+// move's serial.
+struct Shortage {
+  int32_t loc = 0, shape = -1;
+  int64_t serial = -1;
+};
+
+// A space ran short.  With nothing pending there is nothing to reclaim (the
+// caller's re-check fails).  With a wait callback, every pending move issued
+// up to now is completed once the callback confirms its copy finished, as
+// _reclaim_gpu/cpu_move_blocks do (block_manager.py:410-472).  Without one,
+// a call that may suspend reports the shortage; a resumed call (whose caller
+// has reclaimed already) does not suspend for the same allocation again, as
+// the reference reclaims once per _get_free_blocks (:510-519,547-560).
+int on_short(aegkv_block_manager* bm, int32_t loc, int32_t shape, bool may_suspend,
+             Shortage* sh) {
+  std::deque<MoveEvent>& q = move_queue(bm, loc, shape);
+  if (q.empty()) return AEGKV_OK;
+  const int64_t target = q.back().serial;
+  if (bm->wait) {
+    if (bm->wait(bm->wait_ctx, loc, shape, target) != 0) return AEGKV_OK;
+    while (!q.empty() && q.front().serial <= target) {
+      MoveEvent ev = std::move(q.front());
+      q.pop_front();
+      if (is_gpu(loc)) reclaim_gpu_once(bm->gpu[loc], ev);
+      else reclaim_cpu_once(bm, ev);
+    }
+    if (!is_gpu(loc)) reclaim_cpu_slabs(bm);
+    return AEGKV_OK;
+  }
+  if (!may_suspend) return AEGKV_OK;
+  sh->loc = loc;
+  sh->shape = shape;
+  sh->serial = target;
+  return AEGKV_RECLAIM_PENDING;
+}
+
+// _get_free_blocks (block_manager.py:498-582).  On a shortage: on_short, then
+// one re-check (AEGKV_ERR_NO_SPACE, the reference's ResourceWarning).
+// AEGKV_RECLAIM_PENDING takes nothing.
 int get_free_blocks(aegkv_block_manager* bm, int64_t n, int32_t loc, int32_t shape,
-                    std::vector<int64_t>* out) {
+                    std::vector<int64_t>* out, bool may_suspend, Shortage* sh) {
   out->clear();
   if (n <= 0) return AEGKV_OK;
   if (is_gpu(loc)) {
@@ -163,8 +221,8 @@ int get_free_blocks(aegkv_block_manager* bm, int64_t n, int32_t loc, int32_t sha
     if (it == bm->gpu.end()) return AEGKV_ERR_INVALID_ARG;
     GpuSpace& g = it->second;
     if ((int64_t)g.free.size() < n) {
-      int rc = reclaim_moves(bm, loc, shape);
-      if (rc && rc != AEGKV_ERR_NO_SPACE) return rc;
+      const int rc = on_short(bm, loc, shape, may_suspend, sh);
+      if (rc) return rc;
       if ((int64_t)g.free.size() < n) return AEGKV_ERR_NO_SPACE;
     }
     out->assign(g.free.begin(), g.free.begin() + n);
@@ -185,8 +243,8 @@ int get_free_blocks(aegkv_block_manager* bm, int64_t n, int32_t loc, int32_t sha
     return false;
   };
   if (!ensure(n - (int64_t)fl.size())) {
-    int rc = reclaim_moves(bm, loc, shape);
-    if (rc && rc != AEGKV_ERR_NO_SPACE) return rc;
+    const int rc = on_short(bm, loc, shape, may_suspend, sh);
+    if (rc) return rc;
     if (!ensure(n - (int64_t)fl.size())) return AEGKV_ERR_NO_SPACE;
   }
   while ((int64_t)fl.size() < n) {
@@ -207,31 +265,185 @@ int get_free_blocks(aegkv_block_manager* bm, int64_t n, int32_t loc, int32_t sha
   return AEGKV_OK;
 }
 
-// Undo the table updates of a move that failed part-way: the target blocks
-// return to the head of their free list in their original order (the latest
-// taken first), the tables get their old blocks back.  Reclaims the failed call
-// triggered stay done; slabs it opened stay with the shape (their blocks free).
-void undo_moves(aegkv_block_manager* bm, int32_t target, int32_t shape, int32_t source) {
-  const uint64_t bb = block_bytes_of(bm, shape);
-  size_t off = bm->last_src.size();
-  for (size_t k = bm->last_reqs.size(); k-- > 0;) {
-    Table& tab = bm->tables[bm->last_reqs[k]];
-    const size_t nb = tab.blocks.size();
-    off -= nb;
-    if (is_gpu(target)) {
-      auto& fl = bm->gpu[target].free;
-      fl.insert(fl.begin(), tab.blocks.begin(), tab.blocks.end());
-    } else {
-      auto& fl = bm->cpu_free[shape];
-      fl.insert(fl.begin(), tab.blocks.begin(), tab.blocks.end());
-      for (int64_t b : tab.blocks) bm->slab_usage[slab_of(bm, b, bb)] -= 1;
-    }
-    tab.blocks.assign(bm->last_src.begin() + off, bm->last_src.begin() + off + nb);
-    tab.location = source;
+// Blocks go back to a space: at the head of its free list in their order
+// (undoing an allocation) or at the tail (a free).
+void give_back(aegkv_block_manager* bm, int32_t loc, int32_t shape, const int64_t* b, size_t n,
+               bool at_head) {
+  if (n == 0) return;
+  if (is_gpu(loc)) {
+    auto& fl = bm->gpu[loc].free;
+    fl.insert(at_head ? fl.begin() : fl.end(), b, b + n);
+    return;
   }
-  bm->last_src.clear();
-  bm->last_dst.clear();
-  bm->last_reqs.clear();
+  const uint64_t bb = block_bytes_of(bm, shape);
+  auto& fl = bm->cpu_free[shape];
+  fl.insert(at_head ? fl.begin() : fl.end(), b, b + n);
+  for (size_t k = 0; k < n; ++k) bm->slab_usage[slab_of(bm, b[k], bb)] -= 1;
+}
+
+void set_busy(aegkv_block_manager* bm, const PendingOp& op, bool on) {
+  for (int64_t id : op.ids) {
+    if (on) bm->busy.insert(id);
+    else bm->busy.erase(id);
+  }
+}
+
+// A request a suspended move had already assigned was freed meanwhile: the
+// free returned its target blocks, so its pair leaves the move and its source
+// blocks are freed at the source (nothing was copied yet).
+void drop_freed(aegkv_block_manager* bm, PendingOp& op) {
+  std::vector<int64_t> src, dst, moved, sizes;
+  size_t off = 0;
+  for (size_t k = 0; k < op.moved.size(); ++k) {
+    const size_t nb = (size_t)op.sizes[k];
+    if (bm->tables.count(op.moved[k])) {
+      src.insert(src.end(), op.src.begin() + off, op.src.begin() + off + nb);
+      dst.insert(dst.end(), op.dst.begin() + off, op.dst.begin() + off + nb);
+      moved.push_back(op.moved[k]);
+      sizes.push_back((int64_t)nb);
+    } else {
+      give_back(bm, op.source, op.mshape, op.src.data() + off, nb, false);
+    }
+    off += nb;
+  }
+  op.src.swap(src);
+  op.dst.swap(dst);
+  op.moved.swap(moved);
+  op.sizes.swap(sizes);
+}
+
+// Undo a move that failed or was cancelled: the target blocks return to the
+// head of their free list in their original order (the latest taken first),
+// the tables get their old blocks back.  Reclaims the call triggered stay done;
+// slabs it opened stay with the shape (their blocks free).
+void rollback_move(aegkv_block_manager* bm, PendingOp& op) {
+  drop_freed(bm, op);
+  size_t off = op.src.size();
+  for (size_t k = op.moved.size(); k-- > 0;) {
+    const size_t nb = (size_t)op.sizes[k];
+    off -= nb;
+    Table& tab = bm->tables[op.moved[k]];
+    give_back(bm, op.target, op.mshape, tab.blocks.data(), tab.blocks.size(), true);
+    tab.blocks.assign(op.src.begin() + off, op.src.begin() + off + nb);
+    tab.location = op.source;
+  }
+  op.src.clear();
+  op.dst.clear();
+  op.moved.clear();
+  op.sizes.clear();
+}
+
+// The loop of move_requests (block_manager.py:797-832) from request op.next:
+// each request not yet at the target gets target blocks and its table moves.
+int run_move(aegkv_block_manager* bm, PendingOp& op) {
+  std::vector<int64_t> got;
+  for (; op.next < op.ids.size(); ++op.next) {
+    auto t = bm->tables.find(op.ids[op.next]);
+    if (t == bm->tables.end()) continue;  // freed while the call was suspended
+    Table& tab = t->second;
+    if (tab.location == op.target) continue;
+    if (tab.location != op.source || tab.shape != op.mshape) return AEGKV_ERR_IN_USE;
+    Shortage sh;
+    const int rc = get_free_blocks(bm, (int64_t)tab.blocks.size(), op.target, op.mshape, &got,
+                                   !op.reclaimed, &sh);
+    if (rc == AEGKV_RECLAIM_PENDING) {
+      op.loc = sh.loc;
+      op.shape = sh.shape;
+      op.serial = sh.serial;
+      return rc;
+    }
+    op.reclaimed = false;
+    if (rc) return rc;
+    op.src.insert(op.src.end(), tab.blocks.begin(), tab.blocks.end());
+    op.dst.insert(op.dst.end(), got.begin(), got.end());
+    op.moved.push_back(op.ids[op.next]);
+    op.sizes.push_back((int64_t)got.size());
+    tab.blocks = got;
+    tab.location = op.target;
+  }
+  return AEGKV_OK;
+}
+
+// The end of move_requests (:834-872): the lists for the swap call, and the
+// pending move whose source blocks are reclaimed once its copy is done.
+void finish_move(aegkv_block_manager* bm, PendingOp& op, int64_t* serial, int64_t* n_blocks,
+                 int32_t* is_swap_in, int32_t* engine) {
+  bm->last_src = op.src;
+  bm->last_dst = op.dst;
+  bm->last_reqs = op.moved;
+  *is_swap_in = is_gpu(op.target) ? 1 : 0;
+  *engine = is_gpu(op.target) ? op.target : op.source;
+  *serial = -1;
+  *n_blocks = (int64_t)op.src.size();
+  if (op.moved.empty()) return;
+  MoveEvent ev{bm->next_serial++, op.mshape, op.source, op.target, op.src};
+  if (is_gpu(op.source)) {
+    GpuSpace& g = bm->gpu[op.source];
+    g.moving += (int64_t)ev.source_blocks.size();
+    g.moves.push_back(std::move(ev));
+  } else {
+    bm->cpu_moving[op.mshape] += (int64_t)ev.source_blocks.size();
+    bm->cpu_moves[op.mshape].push_back(std::move(ev));
+  }
+  *serial = bm->next_serial - 1;
+}
+
+// Hand out an allocation (:680-694): new requests get a table, known ones
+// grow at the tail.
+void assign_allocation(aegkv_block_manager* bm, const PendingOp& op,
+                       const std::vector<int64_t>& got) {
+  int64_t cur = 0;
+  for (size_t i = 0; i < op.ids.size(); ++i) {
+    const int64_t c = op.counts[i];
+    auto t = bm->tables.find(op.ids[i]);
+    if (t == bm->tables.end()) {
+      if (op.had[i]) continue;  // freed while the call was suspended: nothing for it
+      Table tab{op.engine, op.mshape,
+                std::vector<int64_t>(got.begin() + cur, got.begin() + cur + c)};
+      bm->tables.emplace(op.ids[i], std::move(tab));
+    } else {
+      t->second.blocks.insert(t->second.blocks.end(), got.begin() + cur, got.begin() + cur + c);
+    }
+    cur += c;
+  }
+}
+
+// The batched allocation of a (new or resumed) allocate call.
+int run_allocate(aegkv_block_manager* bm, PendingOp& op) {
+  op.total = 0;
+  for (size_t i = 0; i < op.ids.size(); ++i) {
+    auto t = bm->tables.find(op.ids[i]);
+    if (t == bm->tables.end() && op.had[i]) op.counts[i] = 0;
+    if (t != bm->tables.end() && t->second.location != op.engine) return AEGKV_ERR_IN_USE;
+    op.total += op.counts[i];
+  }
+  std::vector<int64_t> got;
+  Shortage sh;
+  const int rc = get_free_blocks(bm, op.total, op.engine, op.mshape, &got, !op.reclaimed, &sh);
+  if (rc == AEGKV_RECLAIM_PENDING) {
+    op.loc = sh.loc;
+    op.shape = sh.shape;
+    op.serial = sh.serial;
+    return rc;
+  }
+  if (rc) return rc;
+  assign_allocation(bm, op, got);
+  return AEGKV_OK;
+}
+
+int64_t suspend(aegkv_block_manager* bm, PendingOp&& op) {
+  const int64_t id = bm->next_op++;
+  set_busy(bm, op, true);
+  bm->ops.emplace(id, std::move(op));
+  bm->last_op = id;
+  return id;
+}
+
+bool any_busy(const aegkv_block_manager* bm, const int64_t* ids, int64_t n) {
+  if (bm->busy.empty()) return false;
+  for (int64_t i = 0; i < n; ++i)
+    if (bm->busy.count(ids[i])) return true;
+  return false;
 }
 
 }  // namespace
@@ -270,11 +482,17 @@ int aegkv_bm_define_shape(aegkv_block_manager* bm, int32_t shape, uint64_t block
 
 // register_gpu_space (block_manager.py:300-348).  Unlike the reference, which
 // clears the pending moves of every engine (:321-322) and so strands their
-// source blocks, only this engine's pending GPU moves are dropped.
+// source blocks, only this engine's pending GPU moves are dropped.  A space
+// that a suspended call allocates in or moves from/to is in use.
 int aegkv_bm_register_gpu_space(aegkv_block_manager* bm, int32_t engine, int64_t num_max_blocks,
                                 int32_t shape) {
   if (!bm || engine < 0 || num_max_blocks < 0 || block_bytes_of(bm, shape) == 0)
     return AEGKV_ERR_INVALID_ARG;
+  for (auto& kv : bm->ops) {
+    const PendingOp& op = kv.second;
+    if (op.is_move ? (op.target == engine || op.source == engine) : op.engine == engine)
+      return AEGKV_ERR_IN_USE;
+  }
   auto it = bm->gpu.find(engine);
   if (it != bm->gpu.end()) {
     for (auto& kv : bm->tables)
@@ -307,33 +525,24 @@ int aegkv_bm_allocate(aegkv_block_manager* bm, int32_t engine, const int64_t* re
     return AEGKV_ERR_INVALID_ARG;
   auto git = bm->gpu.find(engine);
   if (git == bm->gpu.end()) return AEGKV_ERR_INVALID_ARG;
-  const int32_t shape = git->second.shape;
-  std::vector<int64_t> counts(n);
-  int64_t total = 0;
+  if (any_busy(bm, request_ids, n)) return AEGKV_ERR_IN_USE;
+  PendingOp op;
+  op.engine = engine;
+  op.mshape = git->second.shape;
+  op.ids.assign(request_ids, request_ids + n);
+  op.counts.resize(n);
+  op.had.resize(n);
   for (int64_t i = 0; i < n; ++i) {
     auto t = bm->tables.find(request_ids[i]);
     if (t != bm->tables.end() && t->second.location != engine) return AEGKV_ERR_IN_USE;
     const int64_t have = t == bm->tables.end() ? 0 : (int64_t)t->second.blocks.size();
-    counts[i] = num_blocks_needed[i] - have;
-    if (counts[i] < 0) return AEGKV_ERR_INVALID_ARG;
-    total += counts[i];
+    op.had[i] = t != bm->tables.end();
+    op.counts[i] = num_blocks_needed[i] - have;
+    if (op.counts[i] < 0) return AEGKV_ERR_INVALID_ARG;
   }
-  std::vector<int64_t> got;
-  int rc = get_free_blocks(bm, total, engine, shape, &got);
-  if (rc) return rc;
-  int64_t cur = 0;
-  for (int64_t i = 0; i < n; ++i) {
-    auto t = bm->tables.find(request_ids[i]);
-    if (t == bm->tables.end()) {
-      Table tab{engine, shape, std::vector<int64_t>(got.begin() + cur, got.begin() + cur + counts[i])};
-      bm->tables.emplace(request_ids[i], std::move(tab));
-    } else {
-      t->second.blocks.insert(t->second.blocks.end(), got.begin() + cur,
-                              got.begin() + cur + counts[i]);
-    }
-    cur += counts[i];
-  }
-  return AEGKV_OK;
+  const int rc = run_allocate(bm, op);
+  if (rc == AEGKV_RECLAIM_PENDING) suspend(bm, std::move(op));
+  return rc;
 }
 
 // free_blocks (block_manager.py:696-711).
@@ -343,15 +552,7 @@ int aegkv_bm_free(aegkv_block_manager* bm, int64_t request_id) {
   if (t == bm->tables.end()) return AEGKV_ERR_OUT_OF_RANGE;
   Table tab = std::move(t->second);
   bm->tables.erase(t);
-  if (is_gpu(tab.location)) {
-    auto& fl = bm->gpu[tab.location].free;
-    fl.insert(fl.end(), tab.blocks.begin(), tab.blocks.end());
-  } else {
-    const uint64_t bb = block_bytes_of(bm, tab.shape);
-    auto& fl = bm->cpu_free[tab.shape];
-    fl.insert(fl.end(), tab.blocks.begin(), tab.blocks.end());
-    for (int64_t b : tab.blocks) bm->slab_usage[slab_of(bm, b, bb)] -= 1;
-  }
+  give_back(bm, tab.location, tab.shape, tab.blocks.data(), tab.blocks.size(), false);
   return AEGKV_OK;
 }
 
@@ -381,40 +582,26 @@ int aegkv_bm_move(aegkv_block_manager* bm, const int64_t* request_ids, int64_t n
     any = true;
   }
   if (any && is_gpu(target) && bm->gpu[target].shape != shape) return AEGKV_ERR_INVALID_ARG;
+  if (any_busy(bm, request_ids, n)) return AEGKV_ERR_IN_USE;
   bm->last_src.clear();
   bm->last_dst.clear();
   bm->last_reqs.clear();
-  *serial = -1;
-  *n_blocks = 0;
-  *is_swap_in = is_gpu(target) ? 1 : 0;
-  *engine = is_gpu(target) ? target : cur;
-  if (!any) return AEGKV_OK;
-  std::vector<int64_t> got;
-  for (int64_t i = 0; i < n; ++i) {
-    Table& tab = bm->tables[request_ids[i]];
-    if (tab.location == target) continue;
-    int rc = get_free_blocks(bm, (int64_t)tab.blocks.size(), target, shape, &got);
-    if (rc) {
-      undo_moves(bm, target, shape, cur);
-      return rc;
-    }
-    bm->last_src.insert(bm->last_src.end(), tab.blocks.begin(), tab.blocks.end());
-    bm->last_dst.insert(bm->last_dst.end(), got.begin(), got.end());
-    bm->last_reqs.push_back(request_ids[i]);
-    tab.blocks = got;
-    tab.location = target;
+  PendingOp op;
+  op.is_move = true;
+  op.target = target;
+  op.source = any ? cur : target;
+  op.mshape = shape;
+  if (any) op.ids.assign(request_ids, request_ids + n);
+  const int rc = run_move(bm, op);
+  if (rc == AEGKV_RECLAIM_PENDING) {
+    suspend(bm, std::move(op));
+    return rc;
   }
-  MoveEvent ev{bm->next_serial++, shape, cur, target, bm->last_src};
-  if (is_gpu(cur)) {
-    GpuSpace& g = bm->gpu[cur];
-    g.moving += (int64_t)ev.source_blocks.size();
-    g.moves.push_back(std::move(ev));
-  } else {
-    bm->cpu_moving[shape] += (int64_t)ev.source_blocks.size();
-    bm->cpu_moves[shape].push_back(std::move(ev));
+  if (rc) {
+    rollback_move(bm, op);
+    return rc;
   }
-  *serial = bm->next_serial - 1;
-  *n_blocks = (int64_t)bm->last_src.size();
+  finish_move(bm, op, serial, n_blocks, is_swap_in, engine);
   return AEGKV_OK;
 }
 
@@ -432,6 +619,66 @@ int aegkv_bm_move_ids(const aegkv_block_manager* bm, int64_t* src_ids, int64_t* 
   return AEGKV_OK;
 }
 
+// The call suspended last: its handle, and the space and serial up to which
+// its caller awaits and reclaims the pending moves before resuming it.
+int aegkv_bm_pending(const aegkv_block_manager* bm, int64_t* op, int32_t* location,
+                     int32_t* shape, int64_t* serial) {
+  if (!bm || !op || !location || !shape || !serial) return AEGKV_ERR_INVALID_ARG;
+  auto it = bm->ops.find(bm->last_op);
+  if (it == bm->ops.end()) return AEGKV_ERR_OUT_OF_RANGE;
+  *op = it->first;
+  *location = it->second.loc;
+  *shape = it->second.shape;
+  *serial = it->second.serial;
+  return AEGKV_OK;
+}
+
+// Continue a suspended call at the allocation that ran short (once more, with
+// no second suspension for it).  Outputs as aegkv_bm_move (an allocation sets
+// *serial -1 and *engine to its engine).  AEGKV_RECLAIM_PENDING again when a
+// later request of a move runs short; any other failure undoes the call.
+int aegkv_bm_resume(aegkv_block_manager* bm, int64_t op_id, int64_t* serial, int64_t* n_blocks,
+                    int32_t* is_swap_in, int32_t* engine) {
+  if (!bm || !serial || !n_blocks || !is_swap_in || !engine) return AEGKV_ERR_INVALID_ARG;
+  auto it = bm->ops.find(op_id);
+  if (it == bm->ops.end()) return AEGKV_ERR_OUT_OF_RANGE;
+  PendingOp& op = it->second;
+  op.reclaimed = true;
+  int rc;
+  if (op.is_move) {
+    drop_freed(bm, op);
+    rc = run_move(bm, op);
+    if (rc == AEGKV_RECLAIM_PENDING) {
+      bm->last_op = op_id;
+      return rc;
+    }
+    if (rc) rollback_move(bm, op);
+    else finish_move(bm, op, serial, n_blocks, is_swap_in, engine);
+  } else {
+    rc = bm->gpu.count(op.engine) && bm->gpu[op.engine].shape == op.mshape
+             ? run_allocate(bm, op) : AEGKV_ERR_IN_USE;
+    *serial = -1;
+    *n_blocks = 0;
+    *is_swap_in = 0;
+    *engine = op.engine;
+  }
+  set_busy(bm, op, false);
+  bm->ops.erase(it);
+  return rc;
+}
+
+// Abandon a suspended call (its caller's wait failed): a move is undone; an
+// allocation has taken nothing.
+int aegkv_bm_cancel(aegkv_block_manager* bm, int64_t op_id) {
+  if (!bm) return AEGKV_ERR_INVALID_ARG;
+  auto it = bm->ops.find(op_id);
+  if (it == bm->ops.end()) return AEGKV_ERR_OUT_OF_RANGE;
+  if (it->second.is_move) rollback_move(bm, it->second);
+  set_busy(bm, it->second, false);
+  bm->ops.erase(it);
+  return AEGKV_OK;
+}
+
 // Reclaim the pending moves from `location` (a GPU engine, or the CPU pool of
 // `shape`) whose copies the caller has seen finish: the non-waiting form of
 // _reclaim_gpu/cpu_move_blocks, e.g. at a model switch.
@@ -439,7 +686,7 @@ int aegkv_bm_complete_moves(aegkv_block_manager* bm, int32_t location, int32_t s
                             int64_t up_to_serial) {
   if (!bm) return AEGKV_ERR_INVALID_ARG;
   if (is_gpu(location) && bm->gpu.find(location) == bm->gpu.end()) return AEGKV_ERR_INVALID_ARG;
-  std::deque<MoveEvent>& q = is_gpu(location) ? bm->gpu[location].moves : bm->cpu_moves[shape];
+  std::deque<MoveEvent>& q = move_queue(bm, location, shape);
   while (!q.empty() && q.front().serial <= up_to_serial) {
     MoveEvent ev = std::move(q.front());
     q.pop_front();
@@ -447,6 +694,32 @@ int aegkv_bm_complete_moves(aegkv_block_manager* bm, int32_t location, int32_t s
     else reclaim_cpu_once(bm, ev);
   }
   if (!is_gpu(location)) reclaim_cpu_slabs(bm);
+  return AEGKV_OK;
+}
+
+// One pending move whose copy has finished, wherever it sits in its queue
+// (_reclaim_blocks' per-event callback, :384-406); no slab pass.  A move that
+// is no longer pending is not an error.
+int aegkv_bm_complete_move(aegkv_block_manager* bm, int32_t location, int32_t shape,
+                           int64_t serial) {
+  if (!bm) return AEGKV_ERR_INVALID_ARG;
+  if (is_gpu(location) && bm->gpu.find(location) == bm->gpu.end()) return AEGKV_ERR_INVALID_ARG;
+  std::deque<MoveEvent>& q = move_queue(bm, location, shape);
+  for (auto it = q.begin(); it != q.end(); ++it) {
+    if (it->serial != serial) continue;
+    MoveEvent ev = std::move(*it);
+    q.erase(it);
+    if (is_gpu(location)) reclaim_gpu_once(bm->gpu[location], ev);
+    else reclaim_cpu_once(bm, ev);
+    break;
+  }
+  return AEGKV_OK;
+}
+
+// _reclaim_cpu_slabs (:474-496), run once after a CPU reclaim.
+int aegkv_bm_reclaim_slabs(aegkv_block_manager* bm) {
+  if (!bm) return AEGKV_ERR_INVALID_ARG;
+  reclaim_cpu_slabs(bm);
   return AEGKV_OK;
 }
 

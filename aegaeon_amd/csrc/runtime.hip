@@ -160,7 +160,8 @@ const char* aegkv_strerror(int code) {
     case AEGKV_ERR_WORKSPACE: return "aegkv: workspace or staging buffer too small";
     case AEGKV_ERR_RUNTIME: return "aegkv: a HIP runtime query failed while sizing the call";
     case AEGKV_ERR_NO_SPACE: return "aegkv: not enough free blocks after reclaiming moves";
-    case AEGKV_ERR_IN_USE: return "aegkv: request lives elsewhere, or the space still holds requests";
+    case AEGKV_ERR_IN_USE: return "aegkv: request lives elsewhere, is held by a suspended call, or the space still holds requests";
+    case AEGKV_RECLAIM_PENDING: return "aegkv: the call is suspended until pending moves are reclaimed (aegkv_bm_pending / aegkv_bm_resume)";
     case AEGKV_ERR_SCRATCH: return "aegkv: the call needs a larger workspace than the 32 MiB the no-allocation entry point holds";
     default: break;
   }

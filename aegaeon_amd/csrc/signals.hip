@@ -109,6 +109,16 @@ int aegkv_signal_set(void* word, uint64_t value, aegkv_stream_t stream) {
   return AEGKV_OK;
 }
 
+// The current value of a word, for a host that polls a move (the reference's
+// cudaEventQuery on a rebuilt event): a copy on the caller's stream, waited for.
+int aegkv_signal_read(const void* word, uint64_t* value, aegkv_stream_t stream) {
+  if (!word || !value || (reinterpret_cast<uintptr_t>(word) & 7)) return AEGKV_ERR_INVALID_ARG;
+  AEGKV_HIP_TRY(hipMemcpyAsync(value, word, sizeof(uint64_t), hipMemcpyDeviceToHost,
+                               (hipStream_t)stream));
+  AEGKV_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+  return AEGKV_OK;
+}
+
 int aegkv_signal_wait(const void* word, uint64_t value, uint64_t timeout_us, uint32_t* timed_out,
                       aegkv_stream_t stream) {
   if (!word || (reinterpret_cast<uintptr_t>(word) & 7) || timeout_us == 0)
@@ -118,6 +128,18 @@ int aegkv_signal_wait(const void* word, uint64_t value, uint64_t timeout_us, uin
   AEGKV_HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
   if (khz <= 0) return AEGKV_ERR_RUNTIME;
   const uint64_t ticks = timeout_us * (uint64_t)khz / 1000u;
+  // A timeout word in pinned host memory is written through its device
+  // mapping (the same address under unified addressing; asked, not assumed).
+  if (timed_out) {
+    hipPointerAttribute_t attr;
+    AEGKV_HIP_TRY(hipPointerGetAttributes(&attr, timed_out));
+    if (attr.type == hipMemoryTypeHost) {
+      if (!attr.devicePointer) return AEGKV_ERR_INVALID_ARG;
+      timed_out = static_cast<uint32_t*>(attr.devicePointer);
+    } else if (attr.type != hipMemoryTypeDevice) {
+      return AEGKV_ERR_INVALID_ARG;  // pageable host memory: the kernel cannot write it
+    }
+  }
   hipLaunchKernelGGL(signal_wait_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
                      static_cast<const uint64_t*>(word), value, ticks, timed_out);
   AEGKV_HIP_TRY(hipGetLastError());

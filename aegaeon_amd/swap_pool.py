@@ -81,6 +81,8 @@ class SignalArray:
             _lib.check(self._lib.aegkv_signals_create(self.n_words, ctypes.byref(ptr), handle),
                        "signals_create")
         self.ptr, self.handle, self.owned = ptr.value, bytes(handle), True
+        self._read_stream = None
+        _created[self.handle] = self
 
     @classmethod
     def open(cls, handle: bytes, device) -> "SignalArray":
@@ -95,6 +97,7 @@ class SignalArray:
                                                     ctypes.byref(n)), "signals_open")
         self.ptr, self.handle, self.owned = ptr.value, bytes(handle), False
         self.n_words = int(n.value)
+        self._read_stream = None
         return self
 
     def word(self, i: int) -> int:
@@ -110,13 +113,29 @@ class SignalArray:
         _lib.check(self._lib.aegkv_signal_set(self.word(i), int(value), stream.cuda_stream),
                    "signal_set")
 
+    def read(self, i: int) -> int:
+        """The current value of word ``i``, read from the host (a copy on a
+        stream of this array's own, so no other work is waited for)."""
+        word = self.word(i)
+        if self._read_stream is None:
+            self._read_stream = torch.cuda.Stream(device=self.device)
+        value = ctypes.c_uint64()
+        with torch.cuda.device(self.device):
+            _lib.check(self._lib.aegkv_signal_read(word, ctypes.byref(value),
+                                                   self._read_stream.cuda_stream), "signal_read")
+        return int(value.value)
+
     def wait(self, stream: torch.cuda.Stream, i: int, value: int, timed_out: torch.Tensor,
              timeout_s: float = 120.0) -> None:
         """``stream``'s later work waits until word ``i`` >= ``value`` (or the
-        timeout, which sets the int32 device word ``timed_out``)."""
-        if not (timed_out.is_cuda and timed_out.device == stream.device
+        timeout, which sets the int32 word ``timed_out``: pinned host memory,
+        which the host reads without synchronising, or a word on the stream's
+        GPU)."""
+        on_gpu = timed_out.is_cuda and timed_out.device == stream.device
+        if not ((on_gpu or (not timed_out.is_cuda and timed_out.is_pinned()))
                 and timed_out.dtype == torch.int32 and timed_out.numel() >= 1):
-            raise ValueError("timed_out must be an int32 tensor on the stream's GPU")
+            raise ValueError("timed_out must be an int32 tensor in pinned host memory or on "
+                             "the stream's GPU")
         _lib.check(self._lib.aegkv_signal_wait(self.word(i), int(value),
                                                max(1, int(timeout_s * 1e6)),
                                                timed_out.data_ptr(), stream.cuda_stream),
@@ -131,6 +150,7 @@ class SignalArray:
                 rc = (self._lib.aegkv_signals_destroy if self.owned
                       else self._lib.aegkv_signals_close)(self.ptr)
             self.ptr = 0
+            _created.pop(self.handle, None)
             _lib.check(rc, "signals_close")
 
 
@@ -142,19 +162,32 @@ def reduce_event(array: SignalArray, word: int, serial: int) -> EventHandle:
 
 
 _opened: Dict[bytes, SignalArray] = {}
+_created: Dict[bytes, SignalArray] = {}   # this process's own arrays, by handle
 
 
 def rebuild_event(handle: EventHandle) -> Optional[Tuple[SignalArray, int, int]]:
     """utils.py:318-331: ``(array, word, serial)`` to wait on, opening the
-    exporter's array once per process; None for a handle this process
-    exported (the caller then waits on its own event)."""
+    exporter's array once per process.  A handle this process exported is
+    served by its own array (a process never opens its own); None when that
+    array has been closed."""
     device, pid, raw, word, serial = handle
     if pid == os.getpid():
-        return None
+        arr = _created.get(bytes(raw))
+        return None if arr is None else (arr, int(word), int(serial))
     arr = _opened.get(raw)
     if arr is None:
         arr = _opened[raw] = SignalArray.open(raw, torch.device("cuda", device))
     return arr, int(word), int(serial)
+
+
+def query_event(handle: EventHandle) -> bool:
+    """Whether the move behind ``handle`` has finished (the host-side
+    ``cudaEventQuery`` of a rebuilt event, block_manager.py:387-398)."""
+    opened = rebuild_event(handle)
+    if opened is None:
+        raise ValueError("the signal array of this move handle was closed")
+    arr, word, serial = opened
+    return arr.read(word) >= serial
 
 
 def close_opened() -> None:

@@ -30,11 +30,14 @@ With ``interprocess=True`` every move also sets a word of the worker's
 :class:`aegaeon_amd.swap_pool.SignalArray` (one word per swap stream, the
 move's serial), :meth:`export` gives the handle another process waits on
 (the reference's ``reduce_cuda_event``, utils.py:306-315), and a source entry
-may be such a handle from another process: :meth:`swap_blocks` then makes its
-stream wait on that word, or, for a handle this process exported, on the
-request's own last event (``rebuild_cuda_event``, utils.py:318-331;
-worker.py:795-812).  A wait that times out sets :attr:`timed_out`
-(:meth:`check_timeouts`).  A pageable swap space (the shared file of
+may be such a handle: :meth:`swap_blocks` then makes its stream wait on that
+word (``rebuild_cuda_event``, utils.py:318-331; worker.py:795-812), from this
+process's own array when it exported the handle, so the wait needs no request
+id.  A wait that times out sets :attr:`timed_out`, a word of pinned host
+memory; the host checks it without synchronising at every point where it
+treats moves as complete (:meth:`ready_mask`, :meth:`wait_for_moves`,
+:meth:`wait_for_all_move_in` / ``_out``) and raises ``TimeoutError`` there,
+since the work behind the wait ran unordered.  A pageable swap space (the shared file of
 :func:`aegaeon_amd.swap_pool.init_cpu_cache` where it cannot be page-locked)
 is reached through pinned bounce buffers the worker owns.
 """
@@ -75,7 +78,8 @@ class KVSwapWorker:
 
     def __init__(self, kv_cache: torch.Tensor, kv_swap: torch.Tensor,
                  compute_stream: Optional[torch.cuda.Stream] = None,
-                 interprocess: bool = False, bounce_bytes: int = 256 << 20):
+                 interprocess: bool = False, bounce_bytes: int = 256 << 20,
+                 wait_timeout_s: float = 120.0):
         if not kv_cache.is_cuda:
             raise ValueError("kv_cache must be a GPU tensor")
         self.device = kv_cache.device
@@ -84,7 +88,8 @@ class KVSwapWorker:
         self.interprocess = interprocess
         self.signals = swap_pool.SignalArray(2, self.device) if interprocess else None
         self._serial = {True: 0, False: 0}       # per swap stream (word 1: swap-in)
-        self.timed_out = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.timed_out = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.wait_timeout_s = wait_timeout_s  # bound of a wait on a cross-process move
         # one bounce buffer per direction: the two swap streams run concurrently
         self.bounce = None if kv_swap.is_pinned() else {
             d: swap_pool.bounce_buffer(bounce_bytes) for d in (True, False)}
@@ -107,7 +112,7 @@ class KVSwapWorker:
         new_event = torch.cuda.Event()
         self._wait_source_events(stream, request_ids, source_events)
         for e in _events(after):
-            self._wait(stream, e, None)
+            self._wait(stream, e)
         with torch.cuda.stream(stream):
             ops.swap(source_block_ids, target_block_ids, is_swap_in, self.kv_cache,
                      self.kv_swap, bounce=None if self.bounce is None else self.bounce[is_swap_in])
@@ -131,21 +136,19 @@ class KVSwapWorker:
         return swap_pool.reduce_event(self.signals, *event.aegkv_signal)
 
     def check_timeouts(self) -> None:
-        """Raise if a wait on another process's move gave up (synchronises)."""
-        if int(self.timed_out.item()):
+        """Raise if a wait on a cross-process move gave up (a host read of a
+        pinned word: no synchronisation; it reports waits that have ended)."""
+        if int(self.timed_out[0]):
             raise TimeoutError("a wait on another process's move timed out; the work behind it "
                                "ran unordered")
 
-    def _wait(self, stream: torch.cuda.Stream, e, request_id: Optional[int]) -> None:
+    def _wait(self, stream: torch.cuda.Stream, e) -> None:
         if _is_handle(e):
             opened = swap_pool.rebuild_event(e)
-            if opened is None:  # exported by this process: the request's own event
-                evs = self.move_event_table.get(request_id) if request_id is not None else None
-                if evs:
-                    stream.wait_event(evs[-1])
-                return
+            if opened is None:
+                raise ValueError("the signal array of this move handle was closed")
             arr, word, serial = opened
-            arr.wait(stream, word, serial, self.timed_out)
+            arr.wait(stream, word, serial, self.timed_out, self.wait_timeout_s)
             return
         stream.wait_event(e)
 
@@ -153,7 +156,7 @@ class KVSwapWorker:
                             source_events: Iterable[EventLike]) -> None:
         """worker.py:772-815: a request with a move in flight is waited on
         before anything else touches its blocks; the request's own last event
-        stands in when the handle is this worker's."""
+        stands in when its entry holds no event."""
         source_events = list(source_events)
         if len(source_events) != len(request_ids):
             raise ValueError("one source event entry per request")
@@ -163,12 +166,13 @@ class KVSwapWorker:
                 if not evs and self.move_event_table.get(rid):
                     evs = [self.move_event_table[rid][-1]]
                 for e in evs:
-                    self._wait(stream, e, rid)
+                    self._wait(stream, e)
 
     # -- the compute side (worker.py:473-500) -------------------------------------
     def ready_mask(self, request_ids: Sequence[int]) -> List[bool]:
         """A request is ready when it has no move event or its last one has
         completed (a non-blocking query)."""
+        self.check_timeouts()
         mask = []
         for rid in request_ids:
             evs = self.move_event_table.get(rid)
@@ -200,20 +204,27 @@ class KVSwapWorker:
 
     def wait_for_all_move_in(self) -> None:
         self.swap_in_stream.synchronize()
+        self.check_timeouts()
 
     def wait_for_all_move_out(self) -> None:
         self.swap_out_stream.synchronize()
+        self.check_timeouts()
 
     def remote_callable(self, after: EventLike = None):
-        """The block manager's per-engine callable
-        (``remote(method, request_ids, src, dst, source_handles, is_swap_in)``,
-        block_manager.py:833-848): runs :meth:`swap_blocks` and returns its
-        event as the move's handle.  ``after`` is evaluated per call when it
-        is a callable returning events."""
-        def remote(method, request_ids, src, dst, source_handles, is_swap_in):
-            if method != "swap_blocks":
-                raise ValueError(f"unknown worker method {method!r}")
-            extra = after() if callable(after) else after
-            return self.swap_blocks(request_ids, src, dst, source_handles, is_swap_in,
-                                    after=extra)
+        """The block manager's per-engine callable: ``remote("swap_blocks",
+        request_ids, src, dst, source_handles, is_swap_in)`` (block_manager.py:
+        833-848) runs :meth:`swap_blocks` and returns its event as the move's
+        handle; ``remote("clear_request_resource_batched", request_ids)``
+        (block_manager.py:770-776) drops freed requests' events.  ``after`` is
+        evaluated per swap when it is a callable returning events."""
+        def remote(method, *args):
+            if method == "swap_blocks":
+                request_ids, src, dst, source_handles, is_swap_in = args
+                extra = after() if callable(after) else after
+                return self.swap_blocks(request_ids, src, dst, source_handles, is_swap_in,
+                                        after=extra)
+            if method == "clear_request_resource_batched":
+                (request_ids,) = args
+                return self.clear_request_resource_batched(request_ids)
+            raise ValueError(f"unknown worker method {method!r}")
         return remote

@@ -121,7 +121,12 @@ int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, in
  *   aegkv_signal_wait: the stream's later work starts only once
  *     *word >= value (a one-lane kernel polling with system-scope acquire
  *     loads).  After timeout_us of wall-clock time it stops waiting and stores
- *     1 to *timed_out (a DEVICE word, may be NULL), so the kernel always ends.
+ *     1 to *timed_out (a device word or a word of pinned host memory, which
+ *     the host then reads without synchronising; may be NULL), so the kernel
+ *     always ends.
+ *   aegkv_signal_read: *value = the word's current value, read by a copy on
+ *     `stream` that the call waits for (the host-side cudaEventQuery of a
+ *     rebuilt event, block_manager.py:387-398).
  * word must be 8-byte aligned. */
 int aegkv_signals_create(int64_t n_words, void** words, void* ipc_handle);
 int aegkv_signals_destroy(void* words);
@@ -130,6 +135,7 @@ int aegkv_signals_close(void* words);
 int aegkv_signal_set(void* word, uint64_t value, aegkv_stream_t stream);
 int aegkv_signal_wait(const void* word, uint64_t value, uint64_t timeout_us, uint32_t* timed_out,
                       aegkv_stream_t stream);
+int aegkv_signal_read(const void* word, uint64_t* value, aegkv_stream_t stream);
 
 /* ---- block gather / scatter / copy / defrag ----------------------------
  * Device-to-device block copies driven by HOST id lists (the lists the block
@@ -397,14 +403,30 @@ int aegkv_varlen_prefill_attention(void* out, int64_t out_token_stride, const vo
  *     per-slab usage counts (:186-199,528-580), slab reclaim (:474-496);
  *     block ids of a shape are byte offsets / block_bytes (:242-245).
  * A shape is a caller-chosen id (>= 0) with its block bytes.  Locations: an
- * engine id >= 0 or AEGKV_BM_CPU.  When an allocation runs short, the pending
- * moves out of that location are completed as _reclaim_gpu/cpu_move_blocks
- * do (:410-472): the wait callback is called with the highest pending serial,
- * returns 0 once every move up to it has finished copying, and their source
- * blocks are reclaimed; without a callback, or when it returns non-zero, the
- * call fails with AEGKV_ERR_NO_SPACE (the reference's ResourceWarning). */
+ * engine id >= 0 or AEGKV_BM_CPU.
+ *
+ * Reclaim.  When an allocation runs short while moves out of that location
+ * (CPU: of that shape) are pending, the reference awaits them and reclaims
+ * their source blocks (_get_free_blocks -> _reclaim_*_move_blocks,
+ * :498-582, :360-472), polling their events from its event loop.  Here the
+ * call suspends instead (the default): it returns AEGKV_RECLAIM_PENDING,
+ * keeping what it has done (the requests a move has already assigned keep
+ * their new tables, as in the reference); aegkv_bm_pending names the call,
+ * the location/shape and the last pending serial; the caller awaits those
+ * moves, reclaims each with aegkv_bm_complete_move (CPU: then
+ * aegkv_bm_reclaim_slabs once), and calls aegkv_bm_resume, which continues at
+ * the allocation that ran short (re-checked once: AEGKV_ERR_NO_SPACE, the
+ * reference's ResourceWarning, if still short) or aegkv_bm_cancel.  Other
+ * calls may run in between, as other coroutines do in the reference; the
+ * requests of a suspended call are busy (allocate/move on them:
+ * AEGKV_ERR_IN_USE), a free of one drops it from the call.  A caller that
+ * can block may instead install a wait callback (aegkv_bm_set_wait): it is
+ * called at the same point with the last pending serial, returns 0 once every
+ * move up to it has finished copying, and the call reclaims them and goes on
+ * (non-zero: AEGKV_ERR_NO_SPACE). */
 #define AEGKV_ERR_NO_SPACE (-9)      /* not enough free blocks after reclaim     */
 #define AEGKV_ERR_IN_USE (-10)       /* request lives elsewhere / space occupied  */
+#define AEGKV_RECLAIM_PENDING (-12)  /* suspended until pending moves are reclaimed */
 #define AEGKV_BM_CPU (-1)            /* BLOCK_LOCATION_CPU (block_manager.py:96)  */
 
 typedef struct aegkv_block_manager aegkv_block_manager;
@@ -440,6 +462,23 @@ int aegkv_bm_move(aegkv_block_manager* bm, const int64_t* request_ids, int64_t n
 int aegkv_bm_move_ids(const aegkv_block_manager* bm, int64_t* src_ids, int64_t* dst_ids,
                       int64_t cap, int64_t* moved_request_ids, int64_t request_cap,
                       int64_t* n_moved);
+/* The call suspended last (AEGKV_RECLAIM_PENDING): its handle, and the
+ * location/shape and serial up to which the pending moves are awaited. */
+int aegkv_bm_pending(const aegkv_block_manager* bm, int64_t* op, int32_t* location,
+                     int32_t* shape, int64_t* serial);
+/* Continue a suspended allocate/move once those moves are reclaimed; outputs
+ * as aegkv_bm_move (an allocation: serial -1, engine = its engine). */
+int aegkv_bm_resume(aegkv_block_manager* bm, int64_t op, int64_t* serial, int64_t* n_blocks,
+                    int32_t* is_swap_in, int32_t* engine);
+/* Abandon a suspended call: a move is undone, an allocation took nothing. */
+int aegkv_bm_cancel(aegkv_block_manager* bm, int64_t op);
+/* One pending move out of `location` (CPU: of `shape`) whose copy finished:
+ * its source blocks are reclaimed (_reclaim_blocks' per-event callback,
+ * :384-406); no longer pending is not an error. */
+int aegkv_bm_complete_move(aegkv_block_manager* bm, int32_t location, int32_t shape,
+                           int64_t serial);
+/* _reclaim_cpu_slabs (:474-496): empty slabs return to the free-slab stack. */
+int aegkv_bm_reclaim_slabs(aegkv_block_manager* bm);
 /* Reclaim the moves out of `location` (CPU: of `shape`) up to up_to_serial,
  * whose copies the caller has seen finish (_reclaim_blocks, :360-408). */
 int aegkv_bm_complete_moves(aegkv_block_manager* bm, int32_t location, int32_t shape,

@@ -434,3 +434,302 @@ def test_async_api_and_swap_callable():
     n.reset()
     with pytest.raises(AssertionError):
         n.get_block_table(3)
+
+
+# ---------------------------------------------------------------------------
+# awaitable reclaim (block_manager.py:360-472) and the controller's members
+# ---------------------------------------------------------------------------
+class _Copy:
+    """A move's handle whose copy finishes when the test says so (the
+    reference polls cudaEventQuery on it, block_manager.py:387-398)."""
+
+    def __init__(self):
+        self.done = False
+        self.polls = 0
+
+    def query(self):
+        self.polls += 1
+        return self.done
+
+
+def _copies_remote(copies):
+    def remote(method, *args):
+        assert method == "swap_blocks"
+        c = _Copy()
+        copies.append(c)
+        return c
+    return remote
+
+
+def test_reclaim_awaits_while_other_coroutines_run():
+    """An allocation that needs a pending swap-out's blocks awaits its copy
+    without blocking the event loop: another engine allocates and finishes
+    meanwhile; the ids are the oracle's."""
+    copies, log = [], []
+    n = BlockManager(4, 8192)
+    o = BlockManagerOracle(4, 8192)
+    n.register_gpu_space(0, 4, SHAPE_A, _copies_remote(copies))
+    n.register_gpu_space(1, 6, SHAPE_A, _copies_remote(copies))
+    for m in (o,):
+        m.register_gpu_space(0, 4, SHAPE_A)
+        m.register_gpu_space(1, 6, SHAPE_A)
+    r1 = _Req(1, 64)                                      # 4 blocks
+    asyncio.run(n.allocate_blocks_batched(_Batch([r1]), 0))
+    o.allocate_blocks_batched([(1, 4)], 0)
+    assert asyncio.run(n.move_requests(_Batch([r1]), CPU))
+    o.move_requests([1], CPU)
+    assert len(copies) == 1 and not copies[0].done
+
+    async def needs_reclaim():
+        await n.allocate_blocks_batched(_Batch([_Req(2, 32)]), 0)   # 2 blocks: reclaim
+        log.append("engine 0 allocated")
+
+    async def other_engine():
+        for i in range(4):
+            await n.allocate_blocks_batched(_Batch([_Req(10 + i, 16)]), 1)
+            log.append(f"engine 1 step {i}")
+            await asyncio.sleep(0.02)
+        copies[0].done = True                             # the swap-out's copy ends
+
+    async def main():
+        await asyncio.gather(needs_reclaim(), other_engine())
+
+    asyncio.run(main())
+    assert log == [f"engine 1 step {i}" for i in range(4)] + ["engine 0 allocated"]
+    assert copies[0].polls >= 3                           # polled, not blocked on
+    o.allocate_blocks_batched([(2, 2)], 0)
+    o.allocate_blocks_batched([(10 + i, 1) for i in range(4)], 1)
+    for rid in (2, 10, 11, 12, 13):
+        assert n.get_block_table(rid).blocks == o.block_tables[rid].blocks, rid
+    assert n.free_list(0) == o.free_list(0) and n.stats(0) == o.stats(0)
+
+
+def test_mid_move_cpu_reclaim_awaited_matches_oracle():
+    """The oracle's hand-worked sequence (slabs of 30-byte blocks), with every
+    move's copy finishing only after the reclaim has started waiting: the
+    swap-out of [2, 3, 1] runs short at request 1, awaits the swap-in's copy,
+    reclaims its CPU blocks and slab 3, and continues with the same ids."""
+    copies = []
+    n = BlockManager(4, 100)
+    o = BlockManagerOracle(4, 100)
+    n.register_gpu_space(0, 10, SHAPE_C, _copies_remote(copies))
+    o.register_gpu_space(0, 10, SHAPE_C)
+    req = {i: _Req(i, 16 * k) for i, k in ((1, 4), (2, 2), (3, 4))}
+
+    async def finish_later(k, delay=0.03):
+        await asyncio.sleep(delay)
+        copies[k].done = True
+
+    async def run(coro, k):
+        await asyncio.gather(coro, finish_later(k))
+
+    asyncio.run(n.allocate_blocks_batched(_Batch([req[1]]), 0))
+    o.allocate_blocks_batched([(1, 4)], 0)
+    asyncio.run(n.move_requests([req[1]], CPU))       # copy 0: swap-out
+    o.move_requests([1], CPU)
+    asyncio.run(n.move_requests([req[1]], 0))         # copy 1: swap-in
+    o.move_requests([1], 0)
+    # 6 GPU blocks, 2 free: awaits copy 0 (the swap-out) before reclaiming
+    asyncio.run(run(n.allocate_blocks_batched(_Batch([req[2], req[3]]), 0), 0))
+    o.allocate_blocks_batched([(2, 2), (3, 4)], 0)
+    for rid in (2, 3):
+        assert n.get_block_table(rid).blocks == o.block_tables[rid].blocks
+    # the swap-out of [2, 3, 1] needs a CPU reclaim after 2 and 3 took blocks
+    result = {}
+
+    async def move():
+        result["moved"] = await n.move_requests([req[2], req[3], req[1]], CPU)
+
+    asyncio.run(run(move(), 1))
+    r = o.move_requests([2, 3, 1], CPU)
+    assert result["moved"]
+    for rid in (1, 2, 3):
+        t = n.get_block_table(rid)
+        assert (t.location, t.blocks) == (o.block_tables[rid].location,
+                                          o.block_tables[rid].blocks), rid
+    assert n.get_block_table(2).blocks + n.get_block_table(3).blocks + \
+        n.get_block_table(1).blocks == r.target_block_ids == [8, 9, 4, 5, 0, 1, 2, 7, 10, 11]
+    assert n.free_list(CPU, SHAPE_C) == o.free_list(CPU, SHAPE_C) == [12]
+    assert n.stats(CPU, SHAPE_C) == o.stats(CPU, SHAPE_C)
+
+
+def test_second_reclaimer_waits_for_the_first():
+    """Two coroutines run short on the same engine: the first awaits the
+    pending move, the second waits for the first's reclaim (its lock) and then
+    takes the next blocks, in the order the oracle gives sequentially."""
+    copies = []
+    n = BlockManager(8, 8192)
+    o = BlockManagerOracle(8, 8192)
+    n.register_gpu_space(0, 6, SHAPE_A, _copies_remote(copies))
+    o.register_gpu_space(0, 6, SHAPE_A)
+    asyncio.run(n.allocate_blocks_batched(_Batch([_Req(1, 64), _Req(2, 32)]), 0))
+    o.allocate_blocks_batched([(1, 4), (2, 2)], 0)
+    asyncio.run(n.move_requests([_Req(1, 64)], CPU))
+    o.move_requests([1], CPU)
+
+    async def finish():
+        await asyncio.sleep(0.03)
+        copies[0].done = True
+
+    async def main():
+        await asyncio.gather(n.allocate_blocks_batched(_Batch([_Req(3, 32)]), 0),
+                             n.allocate_blocks_batched(_Batch([_Req(4, 16)]), 0), finish())
+
+    asyncio.run(main())
+    o.allocate_blocks_batched([(3, 2)], 0)
+    o.allocate_blocks_batched([(4, 1)], 0)
+    for rid in (3, 4):
+        assert n.get_block_table(rid).blocks == o.block_tables[rid].blocks, rid
+    assert n.free_list(0) == o.free_list(0)
+
+
+def test_suspended_move_holds_its_requests_and_cancel_undoes_it():
+    """While a move waits for a reclaim, its requests are busy (another
+    allocation or move of them is refused); cancelling the waiting coroutine
+    undoes the move, tables and free lists as before it."""
+    copies = []
+    n = BlockManager(1, 6 * 2048)                    # one slab: 6 CPU blocks of SHAPE_A
+    n.register_gpu_space(0, 16, SHAPE_A, _copies_remote(copies))
+    reqs = [_Req(1, 64), _Req(2, 32), _Req(3, 64)]   # 4 + 2 + 4 blocks
+    asyncio.run(n.allocate_blocks_batched(_Batch(reqs), 0))
+    before = {r.request_id: n.get_block_table(r.request_id).blocks for r in reqs}
+    asyncio.run(n.move_requests([reqs[0]], CPU))     # CPU 0..3, copy 0 pending
+    asyncio.run(n.move_requests([reqs[0]], 0))       # swap-in: CPU blocks moving (copy 1)
+    free_cpu = n.free_list(CPU, SHAPE_A)
+    free_gpu = n.free_list(0)
+    tables = {r.request_id: n.get_block_table(r.request_id).blocks for r in reqs}
+
+    async def main():
+        # 2 then 4 CPU blocks: request 2 fits, request 3 waits for copy 1
+        task = asyncio.ensure_future(n.move_requests([reqs[1], reqs[2]], CPU))
+        await asyncio.sleep(0.03)
+        assert not task.done()
+        assert n.get_block_table(2).location == CPU  # moved before the wait
+        with pytest.raises(ValueError):
+            await n.allocate_blocks_batched(_Batch([reqs[1]]), 0)
+        with pytest.raises(ValueError):
+            await n.move_requests([reqs[2]], CPU)
+        task.cancel()
+        with pytest.raises(asyncio.CancelledError):
+            await task
+
+    asyncio.run(main())
+    for r in reqs:
+        t = n.get_block_table(r.request_id)
+        assert t.location == 0 and t.blocks == tables[r.request_id]
+    assert n.free_list(CPU, SHAPE_A) == free_cpu and n.free_list(0) == free_gpu
+    assert before[2] == tables[2] and before[3] == tables[3]
+    copies[1].done = True                             # now the same move goes through
+    assert asyncio.run(n.move_requests([reqs[1], reqs[2]], CPU))
+    assert n.get_block_table(3).location == CPU
+
+
+def test_free_during_suspended_move_drops_the_request():
+    """A request freed while its move waits leaves the move: its target
+    blocks went back with the free, its source blocks are freed at the
+    source, and the swap lists carry only the others."""
+    copies, calls = [], []
+    n = BlockManager(1, 6 * 2048)
+    remote = _copies_remote(copies)
+
+    def recording(method, *args):
+        calls.append(args)
+        return remote(method, *args)
+
+    n.register_gpu_space(0, 16, SHAPE_A, recording)
+    reqs = [_Req(1, 64), _Req(2, 32), _Req(3, 64)]
+    asyncio.run(n.allocate_blocks_batched(_Batch(reqs), 0))
+    asyncio.run(n.move_requests([reqs[0]], CPU))
+    asyncio.run(n.move_requests([reqs[0]], 0))
+    gpu_of_2 = n.get_block_table(2).blocks
+
+    async def main():
+        task = asyncio.ensure_future(n.move_requests([reqs[1], reqs[2]], CPU))
+        await asyncio.sleep(0.03)
+        n.free_blocks(2)                             # moved already, then freed
+        copies[1].done = True
+        assert await task
+
+    asyncio.run(main())
+    ids, src, dst = calls[-1][0], calls[-1][1], calls[-1][2]
+    assert ids == [3] and len(src) == len(dst) == 4
+    assert n.get_block_table(3).location == CPU
+    assert set(gpu_of_2) <= set(n.free_list(0))      # request 2's GPU blocks are free
+    free_cpu = n.free_list(CPU, SHAPE_A)
+    assert len(set(free_cpu)) == len(free_cpu)
+
+
+def test_sync_api_blocks_on_query_handles():
+    """allocate_blocks_by_count (the blocking form) waits on a handle that has
+    only query()/synchronize() and gives the same ids."""
+    class _Ev:
+        def __init__(self):
+            self.synced = False
+
+        def query(self):
+            return self.synced
+
+        def synchronize(self):
+            self.synced = True
+
+    evs = []
+
+    def remote(method, *args):
+        evs.append(_Ev())
+        return evs[-1]
+
+    n = BlockManager(4, 8192)
+    n.register_gpu_space(0, 4, SHAPE_A, remote)
+    n.allocate_blocks_by_count([1], [4], 0)
+    asyncio.run(n.move_requests([_Req(1, 64)], CPU))
+    n.allocate_blocks_by_count([2], [3], 0)
+    assert evs[0].synced and n.get_block_table(2).blocks == [0, 1, 2]
+
+
+def test_controller_members(monkeypatch, tmp_path):
+    """What the reference's controller touches after
+    ``block_manager = BlockManager(cpu_num_slabs, cpu_slab_size_bytes)``
+    (llm.py:383-395, 486-499): ``cudart`` with CudaRTLibrary's methods, the
+    swap space, and ``start_event_loop`` in the controller's asyncio.gather,
+    which logs usage and clears zombies every SLEEP_IN_DAEMON_LOOP seconds."""
+    import aegaeon_amd.block_manager as bmod
+    from aegaeon_amd import swap_pool
+    n = BlockManager(2, 1 << 16)
+    for name in ("cudaSetDevice", "cudaDeviceSynchronize", "cudaDeviceReset",
+                 "cudaGetErrorString", "cudaMalloc", "cudaHostRegister", "cudaFree",
+                 "cudaMemset", "cudaMemcpy", "cudaIpcGetMemHandle", "cudaIpcOpenMemHandle",
+                 "cudaIpcCloseMemHandle", "cudaIpcGetEventHandle", "cudaIpcOpenEventHandle",
+                 "cudaStreamWaitEvent", "cudaEventSynchronize", "cudaEventQuery",
+                 "cudaEventDestroy", "CUDART_CHECK"):
+        assert callable(getattr(n.cudart, name)), name
+    assert n.cudart.cudaGetErrorString(0) == "no error"
+    cache = swap_pool.init_cpu_cache(2, 1 << 16, str(tmp_path / "cpu_cache"))
+    assert cache.numel() * 2 == 2 << 16
+    cleared = []
+    worker_side = []
+
+    def remote(method, *args):
+        worker_side.append((method, args))
+
+    n.register_gpu_space(0, 8, SHAPE_A, remote)
+    monkeypatch.setattr(bmod, "SLEEP_IN_DAEMON_LOOP", 0.01)
+
+    async def engine():
+        await n.allocate_blocks_batched(_Batch([_Req(1, 20), _Req(2, 20)]), 0)
+        n.free_blocks_batched([_Req(1), _Req(2)])
+        await asyncio.sleep(0.05)
+        raise KeyboardInterrupt  # ends the controller's gather
+
+    async def controller():
+        await asyncio.gather(n.start_event_loop(), engine())
+
+    with pytest.raises(KeyboardInterrupt):
+        asyncio.run(controller())
+    assert ("clear_request_resource_batched", ([1, 2],)) in worker_side
+    assert n.zombie_request_ids == []
+    n2 = BlockManager(2, 1 << 16, clear_zombies=cleared.append)
+    n2.register_gpu_space(0, 8, SHAPE_A)
+    n2.allocate_blocks_by_count([5], [1], 0)
+    n2.free_blocks(5)
+    n2.clear_zombie_requests()
+    assert cleared == [[5]] and n2.zombie_request_ids == []

@@ -192,3 +192,100 @@ def test_signal_array_checks_words_and_timeout_word(device):
         arr.close()
     with pytest.raises(ValueError):
         arr.word(0)
+
+
+def test_own_exported_handle_orders_a_later_swap(device):
+    """A move handle this process exported, passed as ``after=`` (no request
+    id), orders the later swap on the other stream behind the held swap-out:
+    the swap-in reads what the swap-out wrote, not the stale host bytes."""
+    cache = torch.zeros((16, *SHAPE), dtype=torch.bfloat16, device=device)
+    host = torch.zeros((8, *SHAPE), dtype=torch.bfloat16, pin_memory=True)
+    worker = KVSwapWorker(cache, host, interprocess=True)
+    cache[0:4] = _seeded(21, 4).to(device).view(torch.bfloat16)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(worker.swap_out_stream):
+        torch.cuda._sleep(int(0.05 * 1.2e9))     # ~50 ms: the swap-out is pending below
+    ev = worker.swap_blocks([1], [0, 1, 2, 3], [4, 5, 6, 7], [None], False)
+    assert not ev.query()
+    handle = worker.export(ev)
+    ev_in = worker.swap_blocks([2], [4, 5, 6, 7], [8, 9, 10, 11], [None], True, after=[handle])
+    ev_in.synchronize()
+    worker.wait_for_all_move_out()
+    assert torch.equal(cache[8:12].view(torch.int16).cpu(), _seeded(21, 4))
+    assert swap_pool.query_event(handle)
+    worker.signals.close()
+
+
+def test_cross_process_wait_timeout_raises_at_host_sync_points(device):
+    """A wait on a move that never completes gives up after its bound (set
+    tiny here, so the wait kernel ends at once) and the next host point that
+    treats moves as complete raises instead of letting the unordered work
+    pass silently."""
+    cache = torch.zeros((8, *SHAPE), dtype=torch.bfloat16, device=device)
+    host = torch.zeros((8, *SHAPE), dtype=torch.bfloat16, pin_memory=True)
+    worker = KVSwapWorker(cache, host, wait_timeout_s=1e-3)
+    arr = swap_pool.SignalArray(2, device)
+    try:
+        never = swap_pool.reduce_event(arr, 1, 7)   # word 1 is never set
+        assert not swap_pool.query_event(never)
+        worker.swap_blocks([3], [0], [1], [None], True, after=[never])
+        with pytest.raises(TimeoutError):
+            worker.wait_for_all_move_in()
+        with pytest.raises(TimeoutError):
+            worker.ready_mask([3])
+        arr.signal(torch.cuda.current_stream(device), 1, 7)
+        torch.cuda.synchronize(device)
+        assert swap_pool.query_event(never) and arr.read(1) == 7
+    finally:
+        torch.cuda.synchronize(device)
+        arr.close()
+
+
+def test_block_manager_reclaim_polls_exported_handles(device):
+    """The block manager's reclaim polls interprocess move handles from the
+    host (``query_event``), without blocking the event loop, and reclaims
+    the source blocks once the held swap-out is done."""
+    import asyncio
+    from aegaeon_amd.block_manager import BLOCK_LOCATION_CPU, BlockManager
+    cache = torch.zeros((8, *SHAPE), dtype=torch.bfloat16, device=device)
+    host = torch.zeros((16, *SHAPE), dtype=torch.bfloat16, pin_memory=True)
+    worker = KVSwapWorker(cache, host, interprocess=True)
+    remote = worker.remote_callable()
+
+    def exporting(method, *args):
+        out = remote(method, *args)
+        return worker.export(out) if method == "swap_blocks" else out
+
+    bm = BlockManager(1, 16 * BB)
+    bm.register_gpu_space(0, 8, SHAPE, exporting)
+
+    class R:
+        def __init__(self, rid, n):
+            self.request_id, self.n, self.is_finished = rid, n, False
+
+        def get_input_len(self):
+            return self.n
+
+        def get_output_len(self):
+            return 0
+
+    r1 = R(1, 16 * 6)
+    asyncio.run(bm.allocate_blocks_batched([r1], 0))
+    with torch.cuda.stream(worker.swap_out_stream):
+        torch.cuda._sleep(int(0.05 * 1.2e9))
+    asyncio.run(bm.move_requests([r1], BLOCK_LOCATION_CPU))
+    ticks = []
+
+    async def other():
+        for _ in range(3):
+            ticks.append(1)
+            await asyncio.sleep(0.001)
+
+    async def main():
+        await asyncio.gather(bm.allocate_blocks_batched([R(2, 16 * 4)], 0), other())
+
+    asyncio.run(main())
+    assert len(ticks) == 3
+    assert bm.get_block_table(2).blocks == [6, 7, 0, 1]
+    torch.cuda.synchronize(device)
+    worker.signals.close()
