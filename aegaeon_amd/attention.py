@@ -413,11 +413,14 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     """vllm-flash-attn's paged decode call for one query token per sequence:
     ``q [B, 1, Hq, D]`` -> ``[B, 1, Hq, D]``.  With a single query token the
     causal mask admits every cached token, so ``causal`` does not change the
-    result.  ``max_seqlen`` (host bound of the attended lengths) defaults to
-    ``block_table.size(1) * block_size``.  With ``k``/``v`` ``[B, 1, Hkv, D]``
+    result.  ``max_seqlen`` (host bound of ``cache_seqlens``) defaults to
+    ``block_table.size(1) * block_size``; longer sequences are attended over
+    their first ``max_seqlen`` tokens.  With ``k``/``v`` ``[B, 1, Hkv, D]``
     the new token is first written at position ``cache_seqlens[b]`` and the
     attention covers ``cache_seqlens[b] + 1`` tokens (flash-attn's kvcache
-    semantics), in one fused call."""
+    semantics), in one fused call; the bound then grows by the new token.  A
+    new token past the table is not written; one past the bound is written but
+    not attended, as the separate append and attention would do."""
     if q.dim() != 4 or q.size(1) != 1:
         raise NotImplementedError("decode only: q must be [B, 1, Hq, D]")
     if cache_seqlens is None or block_table is None:
@@ -433,6 +436,7 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
             raise ValueError("k and v must both be [B, 1, Hkv, D]")
         key, value = k[:, 0], v[:, 0]
         seq_lens = cache_seqlens.to(torch.int32) + 1
+        ms = min(ms + 1, block_table.size(1) * bs)
     o = paged_decode_attention(q.view(B, Hq, D), k_cache, v_cache, block_table, seq_lens,
                                scale, ms, out=None if out is None else out.view(B, Hq, D),
                                key=key, value=value)

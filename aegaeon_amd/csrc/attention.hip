@@ -170,11 +170,14 @@ struct AttnArgs {
   const int32_t* plan_first;
   const int32_t* plan_ids;
   const int32_t* plan_tags;  // per item: new-row tag (see the plan layout)
-  const int32_t* plan_last;  // per sequence: its last block's id
+  const int32_t* plan_last;  // per sequence: the block of its position seq_lens[b] - 1
   // append fused into the call (knew == nullptr: none): the new token's K and
   // V rows of sequence b, kv head h at knew/vnew + b * stride + h * D; the
-  // token is the last of seq_lens[b].  The main kernel reads it from there,
-  // the combine kernel's rows kHeadsPerGroup.. copy it into the cache.
+  // token is the last of seq_lens[b].  The main kernel reads it from there
+  // (when the length is within max_seq_len: a longer sequence is attended over
+  // its first max_seq_len cached tokens, without the new row), the combine
+  // kernel's rows kHeadsPerGroup.. copy it into the cache at its own position
+  // seq_lens[b] - 1, as the separate append would.
   const uint16_t* knew;
   const uint16_t* vnew;
   int64_t knew_bstride, vnew_bstride;  // elements
@@ -195,11 +198,13 @@ inline bool desc_per_sequence(int64_t batch, int64_t n_groups, int64_t n_wg) {
 // int32 (first kv-head group or -1 for an idle workgroup, last group, first
 // item and its sequence, end item in the last group, the batch's first
 // non-empty sequence), the merge descriptors, the block ids and new-row tags
-// of the first 64 items of each workgroup's range, each sequence's last block
-// id (-1 when empty), the block ids of all items in item order (item i =
-// block i - bcum[b] of the sequence b holding it), and their new-row tags
-// (b * 16 + the token offset of the last token in a sequence's last block,
-// -1 for other blocks), which an appending call uses.
+// of the first 64 items of each workgroup's range, the id of the block that
+// holds each sequence's position seq_lens[b] - 1 (-1 when empty or past its
+// table), the block ids of all items in item order (item i = block
+// i - bcum[b] of the sequence b holding it), and their new-row tags (b * 16 +
+// the token offset of the last token in a sequence's last block, -1 for other
+// blocks and for sequences longer than max_seq_len), which an appending call
+// uses.
 struct PlanLayout {
   int64_t wg, desc, first, last, ids, tags, total;
 };
@@ -515,7 +520,8 @@ template <int DT, int D, int NBUF, bool PLANNED, bool FUSED>
 __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s_bcum,
                                              const int32_t* s_len, uint8_t* stage, int4* meta,
                                              int grp, int b0, int i0, int i1, bool have_first,
-                                             int id_first, int tag_first) {
+                                             int id_first, int tag_first,
+                                             const uint32_t* s_over = nullptr) {
   constexpr int KS = D / 32;
   constexpr int DPL = D / 16;
   const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
@@ -552,8 +558,9 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
     } else {
       int b = bh;
       if (s_bcum[b + 1] <= i) b = s_bcum[b + 2] > i ? b + 1 : seq_at(s_bcum, a.batch, i);
-      if constexpr (FUSED)
-        tag = i == s_bcum[b + 1] - 1 ? b * kBlockSize + ((s_len[b] - 1) & (kBlockSize - 1)) : -1;
+      if constexpr (FUSED)  // the new row, unless it lies past the attended range
+        tag = i == s_bcum[b + 1] - 1 && !((s_over[b >> 5] >> (b & 31)) & 1u)
+                  ? b * kBlockSize + ((s_len[b] - 1) & (kBlockSize - 1)) : -1;
       return a.block_tables[(int64_t)b * a.max_blocks + (i - s_bcum[b])];
     }
   };
@@ -702,12 +709,18 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
 
 // Prefix sums of the batch's positions and blocks (lengths clamped to
 // max_seq_len) into LDS: s_cum[batch + 1] (cost units), s_bcum[batch + 1]
-// (blocks), s_len[batch].  Every thread of the 64 * kHeadsPerGroup takes part.
+// (blocks), s_len[batch]; with s_over, bit b set when sequence b's length
+// exceeds max_seq_len (its last token, an appending call's new row, then lies
+// past the attended range).  Every thread of the 64 * kHeadsPerGroup takes
+// part.
 __device__ __forceinline__ void scan_batch(const int32_t* seq_lens, int batch, int max_seq_len,
                                            int32_t* s_cum, int32_t* s_bcum, int32_t* s_len,
-                                           int32_t (*s_wave_tot)[kHeadsPerGroup]) {
+                                           int32_t (*s_wave_tot)[kHeadsPerGroup],
+                                           uint32_t* s_over = nullptr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  if (s_over)
+    for (int w = tid; w < kMaxBatch / 32; w += 64 * kHeadsPerGroup) s_over[w] = 0u;
   // Prefix sums of the batch's positions and blocks: thread t owns sequences
   // [t * per, t * per + per); a wave scan plus the wave totals give each
   // thread its exclusive offsets.
@@ -719,8 +732,10 @@ __device__ __forceinline__ void scan_batch(const int32_t* seq_lens, int batch, i
     // all loads issued before any is used (clamped index, masked after)
 #pragma unroll
     for (int k = 0; k < kScanPerThread; ++k) lens[k] = seq_lens[min(b0 + k, batch - 1)];
+    uint32_t over = 0;  // bit k: sequence b0 + k is longer than max_seq_len
 #pragma unroll
     for (int k = 0; k < kScanPerThread; ++k) {
+      if (k < per && b0 + k < batch && lens[k] > max_seq_len) over |= 1u << k;
       lens[k] = (k < per && b0 + k < batch) ? min(max(lens[k], 0), max_seq_len) : 0;
       cnt += cost_units(lens[k]);
       bcnt += (lens[k] + kBlockSize - 1) / kBlockSize;
@@ -751,6 +766,7 @@ __device__ __forceinline__ void scan_batch(const int32_t* seq_lens, int batch, i
         s_cum[b0 + k] = excl;
         s_bcum[b0 + k] = bexcl;
         s_len[b0 + k] = lens[k];
+        if (s_over && ((over >> k) & 1u)) atomicOr(&s_over[(b0 + k) >> 5], 1u << ((b0 + k) & 31));
         excl += cost_units(lens[k]);
         bexcl += (lens[k] + kBlockSize - 1) / kBlockSize;
       }
@@ -789,6 +805,7 @@ paged_decode_attention_kernel(AttnArgs a) {
   __shared__ int32_t s_wave_tot[2][kHeadsPerGroup];
   __shared__ int32_t s_find[2];
   __shared__ int4 s_meta[kHeadsPerGroup][kMaxStage];
+  __shared__ uint32_t s_over[FUSED ? kMaxBatch / 32 : 1];
   int32_t* s_cum = s_mem;
   int32_t* s_len = s_mem + a.batch + 1;
   int32_t* s_bcum = s_len + a.batch;
@@ -805,7 +822,8 @@ paged_decode_attention_kernel(AttnArgs a) {
     id_first = a.plan_first[(int64_t)blockIdx.x * 128 + lane];
     if constexpr (FUSED) tag_first = a.plan_first[(int64_t)blockIdx.x * 128 + 64 + lane];
   }
-  scan_batch(a.seq_lens, a.batch, a.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot);
+  scan_batch(a.seq_lens, a.batch, a.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot,
+             FUSED && !PLANNED ? s_over : nullptr);
   // Empty sequences have no positions: workgroup b % n_wg writes their zeros.
   for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
     if (s_cum[b + 1] != s_cum[b]) continue;  // uniform over the workgroup
@@ -880,7 +898,7 @@ paged_decode_attention_kernel(AttnArgs a) {
     }
     if (i1 > i0)
       attend_items<DT, D, NBUF, false, FUSED>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0,
-                                              i0, i1, false, 0, -1);
+                                              i0, i1, false, 0, -1, s_over);
     P = q_end;
     __syncthreads();  // s_find is rewritten by the next pass
   }
@@ -910,10 +928,11 @@ struct PlanArgs {
 __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanArgs p) {
   extern __shared__ int32_t s_mem[];
   __shared__ int32_t s_wave_tot[2][kHeadsPerGroup];
+  __shared__ uint32_t s_over[kMaxBatch / 32];
   int32_t* s_cum = s_mem;
   int32_t* s_len = s_mem + p.batch + 1;
   int32_t* s_bcum = s_len + p.batch;
-  scan_batch(p.seq_lens, p.batch, p.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot);
+  scan_batch(p.seq_lens, p.batch, p.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot, s_over);
   const int64_t W = s_cum[p.batch];
   const int items = s_bcum[p.batch];
   const int64_t total = W * p.n_groups;
@@ -984,9 +1003,12 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
     const int b = seq_at(s_bcum, p.batch, i);
     return p.block_tables[(int64_t)b * p.max_blocks + (i - s_bcum[b])];
   };
+  // an appending call's new row: the last attended token, unless the
+  // sequence is longer than the bound (its new row then lies past the range)
   auto tag_of = [&](int i) -> int32_t {
     const int b = seq_at(s_bcum, p.batch, i);
-    return i == s_bcum[b + 1] - 1 ? b * kBlockSize + ((s_len[b] - 1) & (kBlockSize - 1)) : -1;
+    return i == s_bcum[b + 1] - 1 && !((s_over[b >> 5] >> (b & 31)) & 1u)
+               ? b * kBlockSize + ((s_len[b] - 1) & (kBlockSize - 1)) : -1;
   };
   for (int64_t e = gtid; e < (int64_t)p.n_wg * 64; e += gsz) {
     const int w = (int)(e >> 6);
@@ -1001,10 +1023,14 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
     p.ids[i] = id_of(i);
     p.tags[i] = tag_of(i);
   }
-  for (int b = gtid; b < p.batch; b += gsz)
-    p.last[b] = s_len[b] > 0
-                    ? p.block_tables[(int64_t)b * p.max_blocks + (s_len[b] - 1) / kBlockSize]
+  // the block of each sequence's last position (an appending call's new row),
+  // read from its own length also past the bound; -1 without such a block
+  for (int b = gtid; b < p.batch; b += gsz) {
+    const int len = p.seq_lens[b];
+    p.last[b] = len > 0 && (len - 1) / kBlockSize < p.max_blocks
+                    ? p.block_tables[(int64_t)b * p.max_blocks + (len - 1) / kBlockSize]
                     : -1;
+  }
 }
 
 // Merge the pieces of the cut sequence that descriptor blockIdx.x names
@@ -1044,10 +1070,18 @@ __device__ __forceinline__ void copy_new_rows(const AttnArgs& a) {
     const int kv = (int)(rest & 1);
     const int h = (int)((rest >> 1) % a.n_kv_heads);
     const int b = (int)((rest >> 1) / a.n_kv_heads);
-    const int len = min(max(a.seq_lens[b], 0), a.max_seq_len);
-    if (len == 0) continue;
-    const int blk = a.plan_last ? a.plan_last[b]
-                                : a.block_tables[(int64_t)b * a.max_blocks + (len - 1) / kBlockSize];
+    // the new row goes to its own position len - 1 (the append's slot), also
+    // when the length exceeds the attended bound; a table without a block
+    // for it gets nothing, as the append skips a slot outside the pool
+    const int len = a.seq_lens[b];
+    if (len <= 0) continue;
+    int blk;
+    if (a.plan_last) {
+      blk = a.plan_last[b];
+    } else {
+      if ((len - 1) / kBlockSize >= a.max_blocks) continue;
+      blk = a.block_tables[(int64_t)b * a.max_blocks + (len - 1) / kBlockSize];
+    }
     if (blk < 0 || blk >= a.n_blocks) continue;
     const uint16_t* src = (kv ? a.vnew + (int64_t)b * a.vnew_bstride
                               : a.knew + (int64_t)b * a.knew_bstride) + (int64_t)h * D + 8 * chunk;

@@ -576,6 +576,73 @@ def test_fused_append_equals_append_then_attention(device, dtype, Hq, Hkv, D, nw
     _check(to_bits(got), oracle, dtype)
 
 
+@pytest.mark.parametrize("planned", [False, True])
+@pytest.mark.parametrize("nwg", [0, 5])
+def test_fused_append_with_bound_below_longest(device, planned, nwg):
+    """A host bound below the longest lengths: the fused call writes each new
+    row at its own slot and attends the first max_seq_len cached tokens of the
+    longer sequences, exactly as reshape_and_cache_flash followed by the
+    bounded attention (no cached token is overwritten by a clamped row)."""
+    lens = [1, 16, 17, 200, 299, 300, 301, 517, 1100]
+    L, layer, Hq, Hkv, D = 2, 1, 28, 4, 128
+    lens, tables, storage, key, val, q, bt, sl, slots = _fused_case(device, lens, L, Hq, Hkv, D,
+                                                                    "bf16", 61 + nwg)
+    ml = 300
+    scale = 1.0 / math.sqrt(D)
+    two = storage.clone()
+    view2 = two.permute(1, 2, 0, 3, 4, 5)
+    A.reshape_and_cache_flash(key, val, view2[layer, 0], view2[layer, 1], slots)
+    plan = A.DecodePlan(bt, sl, ml, Hkv, nwg) if planned else None
+    ref = A.paged_decode_attention(q, view2[layer, 0], view2[layer, 1], bt, sl, scale, ml,
+                                   n_workgroups=nwg, plan=plan)
+    view = storage.permute(1, 2, 0, 3, 4, 5)
+    got = A.paged_decode_attention(q, view[layer, 0], view[layer, 1], bt, sl, scale, ml,
+                                   n_workgroups=nwg, plan=plan, key=key, value=val)
+    torch.cuda.synchronize()
+    assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    kb = to_bits(two[:, layer, 0])
+    vb = to_bits(two[:, layer, 1])
+    oracle = ko.paged_decode_attention(ko.bits_to_float(to_bits(q), "bf16"),
+                                       ko.bits_to_float(kb, "bf16"), ko.bits_to_float(vb, "bf16"),
+                                       ko.pad_block_tables(tables), np.minimum(lens, ml), scale)
+    _check(to_bits(got), oracle, "bf16")
+
+
+def test_flash_attn_with_kvcache_table_without_room(device):
+    """cache_seqlens at the table's capacity: the new token has no block, so
+    nothing is written and the attention covers the cached tokens, as the
+    default bound (the table's capacity) says; sequences with room append."""
+    ctx = np.asarray([32, 5, 31], dtype=np.int64)        # tables of 2 blocks each
+    rng = np.random.default_rng(62)
+    N = 9
+    ids = rng.permutation(N)[:6]
+    tables = [[int(ids[0]), int(ids[1])], [int(ids[2]), int(ids[3])], [int(ids[4]), int(ids[5])]]
+    storage = to_device_bits(random_bits(rng, (N, 1, 2, 16, 2, 64), "bf16"), "bf16", device)
+    key = to_device_bits(random_bits(rng, (3, 1, 2, 64), "bf16"), "bf16", device)
+    val = to_device_bits(random_bits(rng, (3, 1, 2, 64), "bf16"), "bf16", device)
+    q = to_device_bits(random_bits(rng, (3, 1, 8, 64), "bf16"), "bf16", device)
+    bt = torch.tensor(tables, dtype=torch.int32, device=device)
+    view = storage.permute(1, 2, 0, 3, 4, 5)
+    before = storage.clone()
+    out = A.flash_attn_with_kvcache(q, view[0, 0], view[0, 1], k=key, v=val,
+                                    cache_seqlens=torch.from_numpy(ctx.astype(np.int32)).to(device),
+                                    block_table=bt)
+    torch.cuda.synchronize()
+    kb = to_bits(before[:, 0, 0])
+    vb = to_bits(before[:, 0, 1])
+    with_room = [1, 2]
+    slots = ko.slot_mapping([tables[b] for b in with_room], ctx[with_room], ctx[with_room] + 1)
+    ko.reshape_and_cache_flash(to_bits(key)[with_room, 0], to_bits(val)[with_room, 0], kb, vb,
+                               slots)
+    assert np.array_equal(to_bits(storage[:, 0, 0]), kb)
+    assert np.array_equal(to_bits(storage[:, 0, 1]), vb)
+    ref = ko.paged_decode_attention(ko.bits_to_float(to_bits(q)[:, 0], "bf16"),
+                                    ko.bits_to_float(kb, "bf16"), ko.bits_to_float(vb, "bf16"),
+                                    np.asarray(tables), np.minimum(ctx + 1, 32), 1 / math.sqrt(64))
+    _check(to_bits(out).reshape(3, 8, 64), ref, "bf16")
+
+
 def test_fused_append_batch_above_one_launch(device):
     """2500 sequences (two launches of the unplanned kernel, several rows of
     cache copies in the merge kernel): output and cache equal the two-launch
