@@ -175,13 +175,12 @@ struct AttnArgs {
   // V rows of sequence b, kv head h at knew/vnew + b * stride + h * D; the
   // token is the last of seq_lens[b].  The main kernel reads it from there
   // (when the length is within max_seq_len: a longer sequence is attended over
-  // its first max_seq_len cached tokens, without the new row), the combine
-  // kernel's rows kHeadsPerGroup.. copy it into the cache at its own position
-  // seq_lens[b] - 1, as the separate append would.
+  // its first max_seq_len cached tokens, without the new row), and after its
+  // merges the combine kernel's threads copy it into the cache at its own
+  // position seq_lens[b] - 1, as the separate append would.
   const uint16_t* knew;
   const uint16_t* vnew;
   int64_t knew_bstride, vnew_bstride;  // elements
-  int32_t copy_rows;                   // combine grid rows that copy new rows
   int32_t n_desc;                      // merge descriptors (the combine grid's width)
 };
 
@@ -598,6 +597,26 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
 
   u32x4 qv[KS];
   load_q(bc, qv);
+  // An appending call keeps the new token's K and V rows of the sequence
+  // being computed in registers (lane (j, g): K dims 8g + 32ks, V dims
+  // D/16 * j), loaded when the stream switches to the sequence, and patches
+  // them into the sequence's last block after its ordinary loads; D = 256,
+  // which has no registers to spare, selects the rows per lane at load time.
+  constexpr bool kNewInRegs = FUSED && D <= 128;
+  constexpr int VW = KVRegs<D>::VW;
+  u32x4 knr[kNewInRegs ? KS : 1];
+  uint32_t vnr[kNewInRegs ? VW : 1];
+  auto load_new = [&](int b) {
+    if constexpr (kNewInRegs) {
+      const uint16_t* kp = a.knew + (int64_t)b * a.knew_bstride + (int64_t)h * D + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        knr[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 32 * ks));
+      load_words_global<VW>(a.vnew + (int64_t)b * a.vnew_bstride + (int64_t)h * D + DPL * j,
+                            vnr);
+    }
+  };
+  load_new(bc);
 
   f32x4 acc[DPL];
 #pragma unroll
@@ -624,7 +643,18 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   };
 
   int ic = i0;  // next item to compute
-  auto compute = [&](KVRegs<D>& r, int id) {
+  auto compute = [&](KVRegs<D>& r, int id, int tag) {
+    if constexpr (kNewInRegs) {
+      if (tag >= 0) {  // the sequence's last block holds its new row (uniform)
+        const int noff = tag & (kBlockSize - 1);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) r.k[ks] = j == noff ? knr[ks] : r.k[ks];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int w = 0; w < VW; ++w) r.v[c][w] = 4 * g + c == noff ? vnr[w] : r.v[c][w];
+      }
+    }
     compute_block<DT, D>(r, qv, acc, m, lsum, (ic - first) * kBlockSize, id >= 0 ? len : 0, g,
                          a.scale_log2);
     if (++ic == cend) {  // the piece of sequence bc in this range ends (uniform)
@@ -646,6 +676,7 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
         len = uni(s_len[bc]);
         complete = cend == uni(s_bcum[bc + 1]);  // it starts in range
         load_q(bc, qv);
+        load_new(bc);
 #pragma unroll
         for (int t = 0; t < DPL; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         m = -INFINITY;
@@ -654,18 +685,19 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
     }
   };
 
-  // An appending call swaps the new token's row into each sequence's last
-  // block by lane-wise address selects (no branch around the loads, so the
-  // compiler's wait counts stay exact).
-  // `valid`: the item is in the range (a refill past its end reads nothing;
-  // with an append, it re-reads the range's last block)
+  // Every block is read through raw buffer ranges (no branch around the
+  // loads, so the compiler's wait counts stay exact); `valid`: the item is in
+  // the range (a refill past its end reads nothing).  With D = 256 an
+  // appending call instead swaps the new token's row into each sequence's
+  // last block by lane-wise address selects (a refill past the range then
+  // re-reads the range's last block).
   const uint16_t* kh = FUSED ? a.kc + (int64_t)h * D + (int64_t)j * row + 8 * g : nullptr;
   const uint16_t* vh = FUSED ? a.vc + (int64_t)h * D + (int64_t)(4 * g) * row + DPL * j : nullptr;
   const uint16_t* kn_lane = FUSED ? a.knew + (int64_t)h * D + 8 * g : nullptr;
   const uint16_t* vn_lane = FUSED ? a.vnew + (int64_t)h * D + DPL * j : nullptr;
   auto load_item = [&](KVRegs<D>& r, int id, int tag, bool valid) {
     const int64_t off = (int64_t)max(id, 0) * a.blk_stride;
-    if constexpr (FUSED) {
+    if constexpr (FUSED && !kNewInRegs) {
       const int b = tag >> 4, noff = tag < 0 ? -1 : (tag & (kBlockSize - 1));
       load_block_new<D>(r, kh, vh, off, row, noff, kn_lane + (int64_t)b * a.knew_bstride,
                         vn_lane + (int64_t)b * a.vnew_bstride);
@@ -680,28 +712,28 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   const int n = i1 - i0;
   const int nfull = n - n % NBUF;
   KVRegs<D> buf[NBUF];
-  int ids[NBUF];
+  int ids[NBUF], tags[NBUF];
   unrolled_steps<NBUF>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    int tag = -1;
-    ids[k] = id_at(min(i0 + k, i1 - 1), tag);
-    load_item(buf[k], ids[k], tag, i0 + k < i1);
+    tags[k] = -1;
+    ids[k] = id_at(min(i0 + k, i1 - 1), tags[k]);
+    load_item(buf[k], ids[k], tags[k], i0 + k < i1);
     return false;
   });
   for (int it = 0; it < nfull; it += NBUF) {
     unrolled_steps<NBUF>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
-      compute(buf[k], ids[k]);
-      int tag = -1;
-      ids[k] = id_at(min(i0 + it + k + NBUF, i1 - 1), tag);
-      load_item(buf[k], ids[k], tag, i0 + it + k + NBUF < i1);
+      compute(buf[k], ids[k], tags[k]);
+      tags[k] = -1;
+      ids[k] = id_at(min(i0 + it + k + NBUF, i1 - 1), tags[k]);
+      load_item(buf[k], ids[k], tags[k], i0 + it + k + NBUF < i1);
       return false;
     });
   }
   unrolled_steps<NBUF>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
     if (nfull + k >= n) return true;
-    compute(buf[k], ids[k]);
+    compute(buf[k], ids[k], tags[k]);
     return false;
   });
   flush();
@@ -1049,21 +1081,20 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
 // pieces are raw buffer loads whose piece stride is a scalar offset, which
 // keeps PB = 12 at ~110 VGPRs (PB = 16 measured 1 us slower on the
 // Yi-1.5-9B batch, whose longest sequences have 10-15 pieces; 8 the same).
-// The cache write of an appending call, in the combine's extra grid rows
-// (blockIdx.y >= kHeadsPerGroup), which run beside the merges: the new
-// token's K and V rows of every sequence and kv head go to token
-// (len - 1) % 16 of the sequence's last block, 16 bytes per lane.  The main
-// kernel read those rows from the append's input, so nothing reads the slot
-// before this write.  Blocks outside the pool are skipped, as the attention
-// masks them.
+// The cache write of an appending call, spread over every thread of the
+// combine grid after its merges (extra grid rows for it measured 0.25 us per
+// Qwen2.5-7B layer): the new token's K and V rows of every sequence and kv
+// head go to token (len - 1) % 16 of the sequence's last block, 16 bytes per
+// lane.  The main kernel read those rows from the append's input, so nothing
+// reads the slot before this write.  Blocks outside the pool are skipped, as
+// the attention masks them.
 template <int D>
 __device__ __forceinline__ void copy_new_rows(const AttnArgs& a) {
   constexpr int C = D / 8;  // 16-byte chunks of one kv head's row
   const int64_t total = (int64_t)a.batch * a.n_kv_heads * 2 * C;
-  const int64_t stride = (int64_t)a.copy_rows * gridDim.x * blockDim.x;
+  const int64_t stride = (int64_t)gridDim.x * gridDim.y * blockDim.x;
   const int64_t row = (int64_t)a.n_kv_heads * D;
-  for (int64_t c = ((int64_t)(blockIdx.y - kHeadsPerGroup) * gridDim.x + blockIdx.x) *
-                           blockDim.x + threadIdx.x;
+  for (int64_t c = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
        c < total; c += stride) {
     const int chunk = (int)(c % C);
     const int64_t rest = c / C;
@@ -1092,17 +1123,12 @@ __device__ __forceinline__ void copy_new_rows(const AttnArgs& a) {
   }
 }
 
+
 template <int DT, int D, int KI, int PB>
-__global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(AttnArgs a) {
+__device__ __forceinline__ void merge_pieces(const AttnArgs& a, const int4 d) {
   using E = Elem<DT>;
   constexpr int D4 = D / 4;  // float4 per query head
   constexpr int NT = 64 * kHeadsPerGroup;
-  if (blockIdx.y >= kHeadsPerGroup) {  // uniform: a row of the append's copy
-    copy_new_rows<D>(a);
-    return;
-  }
-  const int4 d = a.desc[blockIdx.x];
-  if (d.x < 0) return;  // uniform over the workgroup
   const int b = d.x, grp = d.y, npieces = d.w;
   const int h = grp * kHeadsPerGroup + blockIdx.y;
   if (h >= a.n_kv_heads) return;
@@ -1165,6 +1191,13 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(
   }
 }
 
+template <int DT, int D, int KI, int PB>
+__global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(AttnArgs a) {
+  const int4 d = a.desc[blockIdx.x];
+  if (d.x >= 0) merge_pieces<DT, D, KI, PB>(a, d);  // uniform over the workgroup
+  if (a.knew) copy_new_rows<D>(a);  // an appending call: the new rows, spread over the grid
+}
+
 // Dynamic LDS of the main kernel: the scan arrays, then (16-byte aligned) the
 // staging records of the four waves.  Sets a.stage_slots and a.stage_off.
 size_t lds_bytes(AttnArgs& a, int max_lds) {
@@ -1204,7 +1237,7 @@ bool positions_fit(int64_t chunk, int64_t nblk_max, int64_t n_groups, int64_t n_
 template <int DT, int D, int KI, int PB>
 int launch_combine(const AttnArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((attention_combine_kernel<DT, D, KI, PB>),
-                     dim3(a.n_desc, kHeadsPerGroup + a.copy_rows), dim3(64 * kHeadsPerGroup), 0,
+                     dim3(a.n_desc, kHeadsPerGroup), dim3(64 * kHeadsPerGroup), 0,
                      stream, a);
   AEGKV_HIP_TRY(hipGetLastError());
   return AEGKV_OK;
@@ -1317,7 +1350,6 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
   a.vnew = static_cast<const uint16_t*>(nr.value);
   a.knew_bstride = nr.key_bstride;
   a.vnew_bstride = nr.value_bstride;
-  a.copy_rows = 0;
   a.n_desc = n_wg;
   if (plan) {
     if (desc_per_sequence(batch, n_groups, n_wg)) a.n_desc = batch * n_groups;
@@ -1353,10 +1385,6 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
     if (nr.key) {
       a.knew = static_cast<const uint16_t*>(nr.key) + (int64_t)c * nr.key_bstride;
       a.vnew = static_cast<const uint16_t*>(nr.value) + (int64_t)c * nr.value_bstride;
-      // enough combine rows that each copy lane moves about one 16-byte chunk
-      const int64_t chunks = (int64_t)a.batch * n_kv_heads * 2 * (head_dim / 8);
-      const int64_t per_row = (int64_t)a.n_desc * 64 * kHeadsPerGroup;
-      a.copy_rows = (int32_t)std::min<int64_t>(64, std::max<int64_t>(1, (chunks + per_row - 1) / per_row));
     }
     const size_t lds = lds_bytes(a, ds->max_lds);
     switch (head_dim) {

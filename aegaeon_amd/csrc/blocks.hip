@@ -3,19 +3,21 @@
 // (aegaeon/ops/swap.cu:25-59).
 //
 // One kernel serves every device-side move.  A block of block_bytes is cut into
-// 16 KiB tiles and the tiles of all blocks are laid end to end, then grouped
-// into chunks of chunk_tiles consecutive tiles; a grid of G workgroups deals
-// the chunks round-robin (workgroup w copies chunks w, w + G, ...), one tile
-// per iteration.  G is 32 per CU (persistent), or one per tile when the
-// source is contiguous and only the destination goes through ids (scatter).  Per tile, each lane issues four non-temporal
-// dwordx4 loads before the four stores (4 KiB in flight per wave, every
-// access a fully coalesced 1 KiB wave row).  The block ids of a workgroup's
-// next tile are loaded together with the current tile's data, so no tile waits
-// on an id load in front of its own loads.  Loads and stores are raw buffer
-// instructions bounded to the tile's valid bytes (no exec branches around
-// memory), which keeps the compiler's wait counts exact: a store waits for its
-// own load only (measured 4% faster on a contiguous 256 MiB copy than the
-// same loop with masked global loads and stores).
+// tiles of 8 KiB and the tiles of all blocks are laid end to end; one
+// short-lived workgroup copies one tile (a grid of at most kMaxCopyGrid
+// workgroups loops over the rest).  A workgroup reads its block's source and
+// destination ids with scalar loads, then each lane issues its kTileUnroll
+// non-temporal dwordx4 loads before its stores (every access a fully coalesced
+// 1 KiB wave row).  Loads and stores are raw buffer instructions bounded to
+// the tile's valid bytes (no exec branches around memory), which keeps the
+// compiler's wait counts exact.
+//
+// Measured on MI355X (same process, 1024 x 12.5 MiB pool, 256 scattered blocks
+// packed, 6.4 GB moved): 8 KiB tiles one per workgroup 6.08 TB/s, 16 KiB 6.01,
+// 32 KiB 5.49, against 5.33 TB/s for the earlier persistent grid (32
+// workgroups per CU walking 16 KiB tiles with the next tile's ids prefetched);
+// a contiguous 1 GiB copy: 16 KiB per workgroup 6.30 TB/s, 8 KiB 6.07, the
+// persistent grid 6.05, hipMemcpyAsync 5.13.
 #include <algorithm>
 #include <cstring>
 #include <numeric>
@@ -23,72 +25,71 @@
 
 #include "aegkv_internal.h"
 
+#ifndef AEGKV_TILE_UNROLL
+#define AEGKV_TILE_UNROLL 2
+#endif
+
 namespace aegkv {
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kCopyThreads = 256;
-constexpr int kCopyUnroll = 4;
-constexpr uint64_t kTileBytes = (uint64_t)kCopyThreads * 16 * kCopyUnroll;  // 16 KiB
-constexpr int kCopyWorkgroupsPerCu = 32;  // measured best of 2..32 with chunks 1..64 tiles
-constexpr int kCopyChunkTiles = 1;  // 0 = one contiguous range per workgroup
-// Largest grid of the per-tile (scatter) launch: HIP bounds a launch to
-// 2^32 - 1 work-items per dimension; beyond this many tiles the kernel's
-// round-robin loop deals the rest to the same workgroups.
+constexpr int kTileUnroll = AEGKV_TILE_UNROLL;  // dwordx4 per lane per tile: 8 KiB tiles
+// Identity copies (no id list on either side) move contiguous bytes: 16 KiB
+// per workgroup measured best there.
+constexpr int kLinearUnroll = 4;
+// Largest grid of one launch: HIP bounds a launch to 2^32 - 1 work-items per
+// dimension; beyond this many tiles the kernel's loop deals the rest to the
+// same workgroups.
 constexpr uint64_t kMaxCopyGrid = 1ull << 23;
 static_assert(kMaxCopyGrid * kCopyThreads <= 0xFFFFFFFFull,
-              "the per-tile copy grid must fit one launch dimension");
+              "the copy grid must fit one launch dimension");
 
 // SRC_IDS / DST_IDS: whether the side is addressed through an id list (else
-// block i of the side is slot i).  Every memory access of the loop is issued
-// unconditionally, so the compiler's wait counts are exact: the stores wait
-// only for their own tile's loads and the loop head only for the next ids.
-template <bool SRC_IDS, bool DST_IDS>
+// block i of the side is slot i).  UNROLL dwordx4 per lane: a tile is
+// kCopyThreads * 16 * UNROLL bytes.  Every value but the lane offsets is
+// uniform over the workgroup (scalar registers).
+template <bool SRC_IDS, bool DST_IDS, int UNROLL>
 __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
     const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
     const int64_t* __restrict__ src_ids, const int64_t* __restrict__ dst_ids,
-    uint64_t block_bytes, uint32_t tiles_per_block, uint64_t n_tiles, uint64_t chunk_tiles) {
-  // every value below is uniform over the workgroup
-  const uint64_t stride = (uint64_t)gridDim.x * chunk_tiles;  // tiles between chunk starts
-  uint64_t tile = (uint64_t)blockIdx.x * chunk_tiles;
-  if (tile >= n_tiles) return;
-  uint64_t chunk_end = min(tile + chunk_tiles, n_tiles);
-  uint64_t i = tile / tiles_per_block;  // block index of the current tile
-  int64_t s = SRC_IDS ? src_ids[i] : (int64_t)i;
-  int64_t d = DST_IDS ? dst_ids[i] : (int64_t)i;
-  while (true) {
-    uint64_t next = tile + 1, next_end = chunk_end;
-    if (next >= chunk_end) {  // first tile of this workgroup's next chunk
-      next = chunk_end - chunk_tiles + stride;
-      next_end = min(next + chunk_tiles, n_tiles);
-    }
-    const bool more = next < n_tiles;
-    const uint64_t ni = more ? next / tiles_per_block : i;
-    const uint64_t base = (tile - i * tiles_per_block) * kTileBytes;
-    const uint32_t bytes = (uint32_t)min(block_bytes - base, kTileBytes);
+    uint64_t block_bytes, uint32_t tiles_per_block, uint64_t n_tiles) {
+  constexpr uint64_t TILE = (uint64_t)kCopyThreads * 16 * UNROLL;
+  for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    const uint64_t i = tile / tiles_per_block;  // block index of the tile
+    const int64_t s = SRC_IDS ? src_ids[i] : (int64_t)i;
+    const int64_t d = DST_IDS ? dst_ids[i] : (int64_t)i;
+    const uint64_t base = (tile - i * tiles_per_block) * TILE;
+    const uint32_t bytes = (uint32_t)min(block_bytes - base, TILE);
     const auto sr = byte_range(src + (uint64_t)s * block_bytes + base, bytes);
     const auto dr = byte_range(dst + (uint64_t)d * block_bytes + base, bytes);
-    u32x4 r[kCopyUnroll];
+    u32x4 r[UNROLL];
 #pragma unroll
-    for (int k = 0; k < kCopyUnroll; ++k)
+    for (int k = 0; k < UNROLL; ++k)
       r[k] = __builtin_amdgcn_raw_buffer_load_b128(sr, (k * kCopyThreads + threadIdx.x) * 16, 0,
                                                    kNt);
-    // the next tile's ids (the same block's again, mostly: an L2 hit), in
-    // flight with the loads above
-    const int64_t ns = SRC_IDS ? src_ids[ni] : (int64_t)ni;
-    const int64_t nd = DST_IDS ? dst_ids[ni] : (int64_t)ni;
 #pragma unroll
-    for (int k = 0; k < kCopyUnroll; ++k)
+    for (int k = 0; k < UNROLL; ++k)
       __builtin_amdgcn_raw_buffer_store_b128(r[k], dr, (k * kCopyThreads + threadIdx.x) * 16, 0,
                                              kNt);
-    if (!more) break;
-    tile = next;
-    chunk_end = next_end;
-    i = ni;
-    s = ns;
-    d = nd;
   }
+}
+
+template <bool SRC_IDS, bool DST_IDS, int UNROLL>
+int launch_tiles(const void* src, void* dst, const int64_t* src_ids, const int64_t* dst_ids,
+                 int64_t n, uint64_t block_bytes, hipStream_t stream) {
+  constexpr uint64_t TILE = (uint64_t)kCopyThreads * 16 * UNROLL;
+  const uint64_t tiles_per_block = (block_bytes + TILE - 1) / TILE;
+  if (tiles_per_block > 0xFFFFFFFFull) return AEGKV_ERR_UNSUPPORTED;
+  const uint64_t n_tiles = tiles_per_block * (uint64_t)n;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, kMaxCopyGrid);
+  hipLaunchKernelGGL((copy_blocks_kernel<SRC_IDS, DST_IDS, UNROLL>), dim3(grid),
+                     dim3(kCopyThreads), 0, stream, static_cast<const uint8_t*>(src),
+                     static_cast<uint8_t*>(dst), src_ids, dst_ids, block_bytes,
+                     (uint32_t)tiles_per_block, n_tiles);
+  AEGKV_HIP_TRY(hipGetLastError());
+  return AEGKV_OK;
 }
 
 }  // namespace
@@ -96,31 +97,21 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
 int launch_copy_blocks(const DeviceState* ds, const void* src, void* dst,
                        const int64_t* src_ids_dev, const int64_t* dst_ids_dev,
                        int64_t n, uint64_t block_bytes, hipStream_t stream) {
+  (void)ds;
   if (n <= 0) return AEGKV_OK;
-  const uint64_t tiles_per_block = (block_bytes + kTileBytes - 1) / kTileBytes;
-  const uint64_t n_tiles = tiles_per_block * (uint64_t)n;
-  // A contiguous source scattered by destination ids (scatter, swap-in) runs
-  // one short-lived workgroup per tile: Llama-2-13B 4096 x 12.5 MiB blocks,
-  // 6.52 TB/s against 6.19 TB/s with the persistent grid.  Pack, copy and defrag
-  // keep the persistent grid (pack measured 5% slower with a tile per
-  // workgroup).
-  const bool per_tile = !src_ids_dev && dst_ids_dev;
-  const uint64_t max_grid =
-      per_tile ? kMaxCopyGrid : (uint64_t)std::max(ds->num_cu, 1) * kCopyWorkgroupsPerCu;
-  const uint64_t chunk = kCopyChunkTiles > 0 ? (uint64_t)kCopyChunkTiles
-                                             : (n_tiles + max_grid - 1) / max_grid;
-  const uint64_t n_chunks = (n_tiles + chunk - 1) / chunk;
-  const uint32_t grid = (uint32_t)std::min<uint64_t>(n_chunks, max_grid);
-  auto kernel = src_ids_dev ? (dst_ids_dev ? copy_blocks_kernel<true, true>
-                                            : copy_blocks_kernel<true, false>)
-                            : (dst_ids_dev ? copy_blocks_kernel<false, true>
-                                           : copy_blocks_kernel<false, false>);
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kCopyThreads), 0, stream,
-                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst),
-                     src_ids_dev, dst_ids_dev, block_bytes, (uint32_t)tiles_per_block,
-                     n_tiles, chunk);
-  AEGKV_HIP_TRY(hipGetLastError());
-  return AEGKV_OK;
+  if (src_ids_dev)
+    return dst_ids_dev
+               ? launch_tiles<true, true, kTileUnroll>(src, dst, src_ids_dev, dst_ids_dev, n,
+                                                        block_bytes, stream)
+               : launch_tiles<true, false, kTileUnroll>(src, dst, src_ids_dev, nullptr, n,
+                                                         block_bytes, stream);
+  if (dst_ids_dev)
+    return launch_tiles<false, true, kTileUnroll>(src, dst, nullptr, dst_ids_dev, n,
+                                                   block_bytes, stream);
+  // identity: one contiguous range of n * block_bytes bytes, copied as a
+  // single block of 16 KiB tiles
+  return launch_tiles<false, false, kLinearUnroll>(src, dst, nullptr, nullptr, 1,
+                                                   (uint64_t)n * block_bytes, stream);
 }
 
 namespace {
