@@ -34,9 +34,7 @@
 // phase later than waves 0-3, so on every SIMD one wave feeds the matrix core
 // while the other runs its softmax.  K and V go from HBM straight into LDS
 // (buffer loads with the LDS bit, no registers), V untransposed, and the
-// P.V operands are read with gfx950's transposing LDS reads.  Since only one
-// wave per SIMD is ever in its softmax, the partner lanes exchange their
-// maxima with v_permlane32_swap instead of an LDS round trip.
+// P.V operands are read with gfx950's transposing LDS reads.
 //
 // Short prompts: two workgroups of four waves per CU, each taking 128 queries;
 // K and V are staged through registers (V transposed on the way into LDS) and
@@ -228,9 +226,7 @@ struct WaveState {
   }
 
   // online softmax of a masked S^T tile into the P^T operands of its four
-  // 16-key steps (kSwap: the partner lanes exchange their maxima with
-  // v_permlane32_swap, see below)
-  template <bool kSwap>
+  // 16-key steps
   __device__ __forceinline__ void softmax(f32x16 (&s)[2], u32x4 (&pb)[4], float scale_log2) {
     float b4[4];  // raw-score max (the scale is positive) over four chains
 #pragma unroll
@@ -241,21 +237,14 @@ struct WaveState {
                    max3(x[e + 6], x[e + 7], x[e + 7]));
     }
     float bm = max3(max3(b4[0], b4[1], b4[2]), b4[3], b4[3]);
-    // the partner lane's max (same query)
-    if (kSwap) {
-      // exchanged between the wave's halves in registers: one
-      // v_permlane32_swap instead of an LDS round trip.  Only where no other
-      // wave of the SIMD can run it at the same time: with two waves of
-      // unsynchronised workgroups per SIMD, both in their softmax, it gave
-      // run-to-run different outputs (also with wait states around it, and
-      // never with one wave per SIMD).
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm),
-                                                       false, false);
-      bm = fmaxf(fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])), bm) * scale_log2;
-    } else {
-      const float pm = __shfl_xor(bm, 32);
-      bm = max3(bm, pm, pm) * scale_log2;
-    }
+    // the partner lane's max (same query), exchanged between the wave's
+    // halves in registers: one v_permlane32_swap instead of the LDS round trip
+    // of a shuffle.  (Both kernels, 20 repeated calls each, also with two
+    // unsynchronised workgroups per CU: bit-identical outputs, and bit-identical
+    // to the shuffle; the four-wave kernel 0-2% faster with it.)
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm),
+                                                     false, false);
+    bm = fmaxf(fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])), bm) * scale_log2;
     if (__builtin_amdgcn_ballot_w64(bm > m + kPfRescaleSlack)) {
       const float mn = fmaxf(m, bm);
       const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 while m = -inf
@@ -285,7 +274,6 @@ struct WaveState {
   // normalise and store the lane's outputs (queries past the end: none)
   __device__ __forceinline__ void store(const PrefillArgs& a, int h, int64_t s0, int len, int qi,
                                         int hh) {
-    // both waves of a SIMD may run this at once: no v_permlane32_swap here
     const float lt = lsum + __shfl_xor(lsum, 32);
     if (qi < len) {
       const float inv = 1.f / lt;
@@ -463,7 +451,7 @@ __device__ __forceinline__ void attend_short(const PrefillArgs& a, uint8_t* lds,
       u32x4 pb[4];
       st.template qk<KPITCH, 0>(lds + (kt & 1) * K_BYTES + col * KPITCH + 16 * hh, sc);
       st.mask(sc, kt * kPfKTile, wq0, qi, len, a.causal, hh);
-      st.template softmax<false>(sc, pb, a.scale_log2);
+      st.softmax(sc, pb, a.scale_log2);
       pv(kt, pb);
     }
     if (more) {
@@ -610,7 +598,7 @@ __device__ __forceinline__ void attend_long(const PrefillArgs& a, uint8_t* lds, 
   };
   auto softmax = [&](int kt, f32x16 (&s)[2], u32x4 (&pb)[4]) {
     st.mask(s, kt * kPfKTile, wq0, qi, len, a.causal, hh);
-    st.template softmax<true>(s, pb, a.scale_log2);  // one softmax wave per SIMD at a time
+    st.softmax(s, pb, a.scale_log2);
   };
   // K_{j+1} and V_j (read from slot 2j + 2 on) are loaded in slot 2j, whose
   // stages were last read in slot 2j - 1
