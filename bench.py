@@ -303,12 +303,22 @@ def bench_pack(args, timer):
     def torch_scatter(i):
         pool.index_copy_(0, dst_dev, staging)
 
+    # the same bytes without id lists: the pool's first blocks copied to the
+    # staging buffer as one contiguous range (the ceiling of a read + write
+    # stream of this size, against which the id-addressed sides are read)
+    front = pool[:wl.n_blocks]
+
+    def contig(i):
+        ops.copy_blocks(front, staging, None, None)
+
     pack(0)
     scatter(0)
+    contig(0)
     torch.cuda.synchronize()
     steps = max(2, args.steps // 40)
     p_ms, _ = timer.run(pack, steps)
     s_ms, _ = timer.run(scatter, steps)
+    c_ms, _ = timer.run(contig, steps)
     tp_ms, _ = timer.run(torch_pack, steps)
     ts_ms, _ = timer.run(torch_scatter, max(1, steps // 4))
     nbytes = wl.pack_bytes()
@@ -316,7 +326,8 @@ def bench_pack(args, timer):
     del pool, staging
     torch.cuda.empty_cache()
     return {"wl": wl, "bytes": nbytes, "pack_ms": p_ms, "scatter_ms": s_ms, "swap": swap,
-            "torch_pack_ms": tp_ms, "torch_scatter_ms": ts_ms}
+            "torch_pack_ms": tp_ms, "torch_scatter_ms": ts_ms, "contig_ms": c_ms,
+            "contig_bytes": 2 * wl.n_blocks * bb}
 
 
 def bench_swap_host(args, wl, pool, staging, src, dst):
@@ -529,7 +540,7 @@ def bench_gather(args, timer):
     """De-page every sequence of the Qwen2.5-7B append batch (one layer, K and
     V) into contiguous [sum(len), Hkv, D] buffers."""
     import torch
-    from aegaeon_amd import attention as A
+    from aegaeon_amd import attention as A, ops
     from aegaeon_amd.workloads import qwen_append_batch
     dev = torch.device("cuda", 0)
     wb = qwen_append_batch(args.seed)
@@ -563,16 +574,29 @@ def bench_gather(args, timer):
         torch.index_select(view[layer, 0], 0, flat_ids, out=tk)
         torch.index_select(view[layer, 1], 0, flat_ids, out=tv)
 
+    # the same rows without a table: one contiguous range of the pool copied
+    # to a buffer of the gather's output size (a read + write stream of the
+    # same bytes)
+    row_bytes = 2 * total * g.row_elems * 2
+    flat = cache.view(torch.uint8).view(-1)[:row_bytes].view(1, row_bytes)
+    flat_out = torch.empty_like(flat)
+
+    def contig(i):
+        ops.copy_blocks(flat, flat_out, None, None, block_bytes=row_bytes)
+
     gather(0)
     torch_gather(0)
+    contig(0)
     torch.cuda.synchronize()
     region_ms, _ = timer.run(gather, max(g.n_layers, args.steps // 4))
     torch_ms, _ = timer.run(torch_gather, max(g.n_layers, args.steps // 8))
+    contig_ms, _ = timer.run(contig, max(g.n_layers, args.steps // 4))
     torch_bytes = 2 * 2 * n_blk * 16 * g.row_elems * 2
     nbytes = 2 * 2 * total * g.row_elems * 2 + 4 * sum(-(-int(x) // 16) for x in sl_np)
-    del cache, tk, tv
+    del cache, tk, tv, flat_out
     torch.cuda.empty_cache()
-    return {"bytes": nbytes, "ms": region_ms, "torch_ms": torch_ms, "torch_bytes": torch_bytes}
+    return {"bytes": nbytes, "ms": region_ms, "torch_ms": torch_ms, "torch_bytes": torch_bytes,
+            "contig_ms": contig_ms, "contig_bytes": 2 * row_bytes}
 
 
 # ------------------------------------------------------------- input preparation
@@ -1163,7 +1187,10 @@ def main(argv=None):
             "us": round(gt["ms"] * 1e3, 2), "bytes": gt["bytes"], "GB/s": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "torch_index_select_whole_blocks_us": round(gt["torch_ms"] * 1e3, 2),
-            "torch_index_select_GB/s": round(gt["torch_bytes"] / (gt["torch_ms"] * 1e-3) / 1e9, 1)}
+            "torch_index_select_GB/s": round(gt["torch_bytes"] / (gt["torch_ms"] * 1e-3) / 1e9, 1),
+            "contiguous_copy_same_bytes_us": round(gt["contig_ms"] * 1e3, 2),
+            "contiguous_copy_same_bytes_GB/s": round(
+                gt["contig_bytes"] / (gt["contig_ms"] * 1e-3) / 1e9, 1)}
     if "pack" in res:
         pk = res["pack"]
         pg = pk["bytes"] / (pk["pack_ms"] * 1e-3) / 1e9
@@ -1178,6 +1205,9 @@ def main(argv=None):
             "torch_index_select_GB/s": round(pk["bytes"] / (pk["torch_pack_ms"] * 1e-3) / 1e9, 1),
             "torch_index_copy_ms": round(pk["torch_scatter_ms"], 3),
             "torch_index_copy_GB/s": round(pk["bytes"] / (pk["torch_scatter_ms"] * 1e-3) / 1e9, 1),
+            "contiguous_copy_same_bytes_ms": round(pk["contig_ms"], 3),
+            "contiguous_copy_same_bytes_GB/s": round(
+                pk["contig_bytes"] / (pk["contig_ms"] * 1e-3) / 1e9, 1),
         }
         sw = pk["swap"]
         if sw is not None:

@@ -664,10 +664,27 @@ def test_fused_append_batch_above_one_launch(device):
     assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
 
 
+def _sampled_oracle(q, kc, vc, tables, lens, sel, scale, dtype):
+    """The float64 oracle for sequences `sel` only, over a cache cut down to
+    their blocks (tables renumbered into it)."""
+    need = sorted({int(x) for b in sel for x in tables[b][:-(-int(lens[b]) // 16)]})
+    where = {x: i for i, x in enumerate(need)}
+    idx = torch.tensor(need, dtype=torch.int64, device=kc.device)
+    k_small = to_bits(kc.index_select(0, idx))
+    v_small = to_bits(vc.index_select(0, idx))
+    sub = ko.pad_block_tables([[where[int(x)] for x in tables[b][:-(-int(lens[b]) // 16)]]
+                               for b in sel])
+    return ko.paged_decode_attention(ko.bits_to_float(to_bits(q)[sel], dtype),
+                                     ko.bits_to_float(k_small, dtype),
+                                     ko.bits_to_float(v_small, dtype), sub, lens[sel], scale)
+
+
 def test_fused_append_qwen_full_batch(device):
     """The Qwen2.5-7B decode batch (128 sequences up to 8192 tokens), planned,
     in the 28-layer storage: the fused call equals the two-launch pattern for
-    every layer of a step that shares one plan."""
+    every layer of a step that shares one plan, and on sampled sequences (the
+    longest, the shortest and six more) it is within the float64 oracle's
+    tolerance."""
     wb = qwen_attention_batch(0)
     g = wb.geometry
     gen = torch.Generator(device=device).manual_seed(53)
@@ -682,6 +699,11 @@ def test_fused_append_qwen_full_batch(device):
     ml = int(wb.seq_lens.max())
     plan = A.DecodePlan(bt, sl, ml, g.n_kv_heads)
     view, view2 = storage.permute(1, 2, 0, 3, 4, 5), two.permute(1, 2, 0, 3, 4, 5)
+    lens = wb.seq_lens.astype(np.int64)
+    order = np.argsort(lens)
+    rng = np.random.default_rng(53)
+    sel = np.unique(np.concatenate([order[:1], order[-1:],
+                                    rng.choice(wb.batch, 6, replace=False)]))
     for layer in range(4):
         q = torch.randn((wb.batch, 28, 128), generator=gen, device=device).to(torch.bfloat16)
         k = torch.randn((wb.batch, 4, 128), generator=gen, device=device).to(torch.bfloat16)
@@ -693,6 +715,9 @@ def test_fused_append_qwen_full_batch(device):
                                        1 / math.sqrt(128), ml, plan=plan, key=k, value=v)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), layer
+        oracle = _sampled_oracle(q, view2[layer, 0], view2[layer, 1], wb.block_tables, lens,
+                                 sel, 1 / math.sqrt(128), "bf16")
+        _check(to_bits(got)[sel], oracle, "bf16")
     assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
 
 
