@@ -9,6 +9,7 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+import sysconfig
 import sys
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
@@ -57,12 +58,29 @@ def _compile(src: str) -> Path:
     return obj
 
 
+def build_listpack() -> Path:
+    """Compile the CPython extension that packs the request lists
+    (``aegaeon_amd/_listpack``, plain C against this interpreter's headers)."""
+    out = CSRC.parent / ("_listpack" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = ["gcc", "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "listpack.c"), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed for listpack.c:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build_library(verbose: bool = False) -> Path:
-    """Compile every source and link ``libaegkv.so``; returns its path."""
+    """Compile every source and link ``libaegkv.so`` (and the list-packing
+    extension); returns the library's path."""
     BUILD_DIR.mkdir(exist_ok=True)
     jobs = min(len(SOURCES), max(1, (os.cpu_count() or 2)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
+        pack = ex.submit(build_listpack)
         objs = list(ex.map(_compile, SOURCES))
+        pack.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)

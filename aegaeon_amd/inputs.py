@@ -13,13 +13,18 @@ host-to-device tensors become one upload and one gfx950 kernel
 """
 from __future__ import annotations
 
-import itertools
 from typing import Dict, List, Sequence, Tuple
 
 import numpy as np
 import torch
 
 from . import _lib
+
+try:
+    from . import _listpack
+except ImportError as e:  # built beside libaegkv.so by csrc/build.py
+    raise ImportError("aegaeon_amd._listpack is not built: run __graft_entry__.build() "
+                      "(aegaeon_amd/csrc/build.py)") from e
 
 BLOCK_SIZE = 16  # aegaeon/aegaeon/config.py:13
 
@@ -46,21 +51,15 @@ def prepare_model_inputs(requests: Sequence[Tuple], block_tables: Sequence[Seque
         raise ValueError("empty batch")  # the reference asserts (worker.py:594)
     if len(block_tables) != len(requests):
         raise ValueError("one block table per request")
-    B = len(requests)
-    # one C-speed pass over each list (the lists are the block manager's)
-    seq = np.fromiter((r[2] for r in requests), dtype=np.int32, count=B)
-    ctx = np.fromiter((r[3] for r in requests), dtype=np.int32, count=B)
-    ntok = np.fromiter((len(r[1]) for r in requests), dtype=np.int64, count=B)
-    if not np.array_equal(ntok, seq.astype(np.int64) - ctx):
-        raise ValueError("a request's tokens must be its seq_len - context_len new tokens")
-    lens = np.fromiter(map(len, block_tables), dtype=np.int64, count=B)
-    offsets = np.zeros(B + 1, dtype=np.int64)
-    np.cumsum(lens, out=offsets[1:])
-    ids = np.fromiter(itertools.chain.from_iterable(block_tables), dtype=np.int32,
-                      count=int(offsets[-1]))
-    tokens = np.fromiter(itertools.chain.from_iterable(r[1] for r in requests), dtype=np.int64,
-                         count=int(ntok.sum()))
-    return prepare_inputs_from_arrays(ids, offsets, seq, ctx, tokens, device, block_size)
+    # the lists read through the CPython API in one pass each (the block
+    # manager's tables, the requests' lengths and new tokens)
+    ids, offsets = _listpack.pack_tables(block_tables)
+    seq, ctx, tokens = _listpack.pack_requests(requests)
+    return prepare_inputs_from_arrays(np.frombuffer(ids, dtype=np.int32),
+                                      np.frombuffer(offsets, dtype=np.int64),
+                                      np.frombuffer(seq, dtype=np.int32),
+                                      np.frombuffer(ctx, dtype=np.int32),
+                                      np.frombuffer(tokens, dtype=np.int64), device, block_size)
 
 
 def prepare_inputs_from_arrays(table_ids: np.ndarray, table_offsets: np.ndarray,
@@ -92,16 +91,13 @@ def prepare_inputs_from_arrays(table_ids: np.ndarray, table_offsets: np.ndarray,
     if tokens.size != T:
         raise ValueError("tokens must hold every request's new tokens")
 
-    i32 = dict(dtype=torch.int32, device=device)
-    i64 = dict(dtype=torch.int64, device=device)
-    bt_out = torch.empty((B, pad_width), **i32)
-    slots = torch.empty(T, **i64)
-    positions = torch.empty(T, **i64)
-    toks = torch.empty(T, **i64)
-    seq_t = torch.empty(B, **i32)
-    ctx_t = torch.empty(B, **i32)
-    qsl = torch.empty(B + 1, **i32)
-    ssl = torch.empty(B + 1, **i32)
+    # the outputs are views of one int32 and one int64 allocation (two
+    # allocator calls per step instead of eight)
+    w32 = torch.empty(B * pad_width + 4 * B + 2, dtype=torch.int32, device=device)
+    w64 = torch.empty(3 * T, dtype=torch.int64, device=device)
+    bt_out = w32[:B * pad_width].view(B, pad_width)
+    seq_t, ctx_t, qsl, ssl = torch.split(w32[B * pad_width:], [B, B, B + 1, B + 1])
+    slots, positions, toks = torch.split(w64, [T, T, T])
     with torch.cuda.device(device):
         rc = _lib.load().aegkv_prepare_inputs(
             _ptr(ids), offsets.ctypes.data, seq.ctypes.data, ctx.ctypes.data, _ptr(tokens), B,
