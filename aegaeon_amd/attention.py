@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import math
 import threading
+import weakref
 from typing import Dict, Optional, Sequence, Tuple
 
 import torch
@@ -403,6 +404,52 @@ def paged_decode_attention(q: torch.Tensor, key_cache: torch.Tensor, value_cache
     return out
 
 
+class _StepPlans:
+    """The decode plan of the tables and lengths a caller passes to every
+    layer of a step.  vLLM's backend hands each layer's
+    flash_attn_with_kvcache the same ``block_table`` and ``cache_seqlens``
+    tensors of the step's metadata (worker.py:694-711, :517-523); the plan
+    built at the first layer serves the others, whose results are bit-identical
+    to unplanned calls.  A cached plan is used only for the very tensor objects
+    it was built from (weak references), at the same version counter (an
+    in-place torch write bumps it) and data pointer, bound, head count and
+    device; anything else builds a new one.  One entry per device: the last
+    step's."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._by_device: Dict[int, tuple] = {}
+
+    @staticmethod
+    def _state(t: torch.Tensor) -> tuple:
+        return (t._version, t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype)
+
+    def get(self, block_table: torch.Tensor, cache_seqlens: torch.Tensor, appending: bool,
+            max_seq_len: int, n_kv_heads: int):
+        """(plan, seq_lens): seq_lens counts the new token when appending;
+        plan is None for a batch too large to plan."""
+        dev = cache_seqlens.device.index
+        key = (self._state(block_table), self._state(cache_seqlens), appending, max_seq_len,
+               n_kv_heads)
+        with self._lock:
+            e = self._by_device.get(dev)
+            if e is not None and e[0]() is block_table and e[1]() is cache_seqlens \
+                    and e[2] == key:
+                return e[3], e[4]
+        seq_lens = cache_seqlens.to(torch.int32) + 1 if appending else cache_seqlens
+        plan = None
+        if 0 < cache_seqlens.numel() <= _PLAN_MAX_BATCH:
+            plan = DecodePlan(block_table, seq_lens, max_seq_len, n_kv_heads)
+        with self._lock:
+            self._by_device[dev] = (weakref.ref(block_table), weakref.ref(cache_seqlens), key,
+                                    plan, seq_lens)
+        return plan, seq_lens
+
+
+_PLAN_MAX_BATCH = 2048  # sequences a plan covers (one launch of the kernels)
+_step_plans = _StepPlans()
+
+
 def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                             k: Optional[torch.Tensor] = None, v: Optional[torch.Tensor] = None,
                             cache_seqlens: Optional[torch.Tensor] = None,
@@ -420,7 +467,10 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     attention covers ``cache_seqlens[b] + 1`` tokens (flash-attn's kvcache
     semantics), in one fused call; the bound then grows by the new token.  A
     new token past the table is not written; one past the bound is written but
-    not attended, as the separate append and attention would do."""
+    not attended, as the separate append and attention would do.  The first
+    call with a step's ``block_table``/``cache_seqlens`` tensors builds their
+    decode plan, which the step's other layers reuse (same tensor objects and
+    versions; see :class:`_StepPlans`)."""
     if q.dim() != 4 or q.size(1) != 1:
         raise NotImplementedError("decode only: q must be [B, 1, Hq, D]")
     if cache_seqlens is None or block_table is None:
@@ -430,16 +480,20 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     bs = k_cache.size(1)
     ms = max_seqlen if max_seqlen is not None else block_table.size(1) * bs
     key = value = None
-    seq_lens = cache_seqlens
     if k is not None or v is not None:
         if k is None or v is None or k.dim() != 4 or k.size(1) != 1 or v.shape != k.shape:
             raise ValueError("k and v must both be [B, 1, Hkv, D]")
         key, value = k[:, 0], v[:, 0]
-        seq_lens = cache_seqlens.to(torch.int32) + 1
         ms = min(ms + 1, block_table.size(1) * bs)
-    o = paged_decode_attention(q.view(B, Hq, D), k_cache, v_cache, block_table, seq_lens,
+    if not (block_table.is_cuda and cache_seqlens.is_cuda and block_table.dim() == 2
+            and block_table.device == q.device and cache_seqlens.device == q.device):
+        raise ValueError("block_table and cache_seqlens must be tensors on q's GPU")
+    plan, seq_lens = _step_plans.get(block_table, cache_seqlens, key is not None, ms,
+                                     k_cache.size(2))
+    o = paged_decode_attention(q.view(B, Hq, D), k_cache, v_cache,
+                               None if plan else block_table, None if plan else seq_lens,
                                scale, ms, out=None if out is None else out.view(B, Hq, D),
-                               key=key, value=value)
+                               plan=plan, key=key, value=value)
     return o.view(B, 1, Hq, D)
 
 

@@ -206,6 +206,22 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
                                  max_len, out=outs[layer], n_workgroups=args.nwg,
                                  workspace=ws, plan=plan[0])
 
+    # vLLM's per-layer call (flash_attn_with_kvcache), as the backend makes it:
+    # every layer of a step passes the step's metadata tensors, which are new
+    # at each step (here: a fresh lengths tensor at layer 0), so the call plans
+    # at the step's first layer and reuses the plan in the others
+    step_lens = [sl]
+    q4 = q.view(g.n_layers, wb.batch, 1, g.n_q_heads, g.head_dim)
+    outs4 = outs.view(g.n_layers, wb.batch, 1, g.n_q_heads, g.head_dim)
+
+    def kvcache_call(i):
+        layer = i % g.n_layers
+        if layer == 0:
+            step_lens[0] = sl.clone()
+        A.flash_attn_with_kvcache(q4[layer], view[layer, 0], view[layer, 1],
+                                  cache_seqlens=step_lens[0], block_table=bt,
+                                  softmax_scale=scale, max_seqlen=max_len, out=outs4[layer])
+
     # The decode step as a layer runs it: the new token's K/V appended, then
     # attention over seq_len tokens (the new one included).  Two launches per
     # layer as vLLM does (reshape_and_cache_flash, then the attention), or
@@ -243,6 +259,11 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
     if not torch.equal(outs, unplanned_out):
         raise RuntimeError("planned and unplanned attention disagree")
     for i in range(g.n_layers):
+        kvcache_call(i)
+    torch.cuda.synchronize()
+    if not torch.equal(outs, unplanned_out):
+        raise RuntimeError("flash_attn_with_kvcache and the unplanned attention disagree")
+    for i in range(g.n_layers):
         two_launch_call(i)
     torch.cuda.synchronize()
     two_out = outs.clone()
@@ -258,7 +279,8 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
     best = {}
     for _ in range(3):
         for name, fn in (("unplanned", layer_call), ("planned", planned_call),
-                         ("two", two_launch_call), ("fused", fused_call)):
+                         ("kvcache", kvcache_call), ("two", two_launch_call),
+                         ("fused", fused_call)):
             ms, _ = timer.run(fn, steps)
             best[name] = min(best.get(name, ms), ms)
     unplanned_ms, region_ms, two_ms, fused_ms = (best[k] for k in
@@ -268,7 +290,7 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
     torch.cuda.empty_cache()
     return {"label": label, "wb": wb, "bytes_per_layer": nbytes, "us_per_layer": region_ms * 1e3,
             "unplanned_us_per_layer": unplanned_ms * 1e3, "two_launch_us": two_ms * 1e3,
-            "fused_us": fused_ms * 1e3}
+            "fused_us": fused_ms * 1e3, "kvcache_us": best["kvcache"] * 1e3}
 
 
 # ------------------------------------------------------------------------ pack / swap
@@ -1169,7 +1191,8 @@ def main(argv=None):
             "us_per_layer": round(t["us_per_layer"], 2),
             "bytes_per_layer": t["bytes_per_layer"], "GB/s": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-            "unplanned_us_per_layer": round(t["unplanned_us_per_layer"], 2)}
+            "unplanned_us_per_layer": round(t["unplanned_us_per_layer"], 2),
+            "flash_attn_with_kvcache_us_per_layer": round(t["kvcache_us"], 2)}
         ops_out["decode_layer_append_then_attention"] = {
             "workload": "the same batch, each layer's new token appended then attended over "
                         "seq_len tokens, one decode plan per step",

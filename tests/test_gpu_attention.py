@@ -800,3 +800,56 @@ def test_one_long_sequence_among_short_ones(device):
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
     assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
+
+
+def test_flash_attn_with_kvcache_reuses_the_step_plan(device):
+    """The vLLM-facing call plans once per step: the layers of a step, which
+    pass the same block_table and cache_seqlens tensors, reuse the plan built
+    at the first (bit-identical to unplanned calls); an in-place edit of the
+    lengths, new tensors with the same contents, or an appending call build a
+    new one."""
+    rng = np.random.default_rng(81)
+    ctx = np.asarray([0, 15, 16, 70, 300, 1], dtype=np.int64)
+    lens, tables, storage, key, val, q, bt, sl, slots = _fused_case(device, ctx + 1, 2, 8, 2, 64,
+                                                                    "bf16", 82)
+    view = storage.permute(1, 2, 0, 3, 4, 5)
+    kc, vc = view[0, 0], view[0, 1]
+    cs = torch.from_numpy(ctx.astype(np.int32)).to(device)
+    q4 = q.view(len(ctx), 1, 8, 64)
+    ms = bt.size(1) * 16
+
+    def unplanned(lengths):
+        return A.paged_decode_attention(q, kc, vc, bt, lengths, 1 / math.sqrt(64), ms)
+
+    out1 = A.flash_attn_with_kvcache(q4, kc, vc, cache_seqlens=cs, block_table=bt)
+    plan1 = A._step_plans._by_device[q.device.index][3]
+    out2 = A.flash_attn_with_kvcache(q4, kc, vc, cache_seqlens=cs, block_table=bt)
+    assert A._step_plans._by_device[q.device.index][3] is plan1 and plan1 is not None
+    ref = unplanned(cs)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(out1.view(-1).view(torch.int16), ref.view(-1).view(torch.int16))
+
+    cs[4] -= 100  # an in-place edit of the step's lengths
+    out3 = A.flash_attn_with_kvcache(q4, kc, vc, cache_seqlens=cs, block_table=bt)
+    assert A._step_plans._by_device[q.device.index][3] is not plan1
+    ref3 = unplanned(cs)
+    torch.cuda.synchronize()
+    assert torch.equal(out3.view(-1).view(torch.int16), ref3.view(-1).view(torch.int16))
+
+    plan3 = A._step_plans._by_device[q.device.index][3]
+    cs2 = cs.clone()  # the next step's tensors, same contents
+    A.flash_attn_with_kvcache(q4, kc, vc, cache_seqlens=cs2, block_table=bt)
+    assert A._step_plans._by_device[q.device.index][3] is not plan3
+
+    # appending: the plan counts the new token; cache and output as the
+    # unplanned appending call leaves them
+    two = storage.clone()
+    v2 = two.permute(1, 2, 0, 3, 4, 5)
+    k4, vv4 = key.view(len(ctx), 1, 2, 64), val.view(len(ctx), 1, 2, 64)
+    got = A.flash_attn_with_kvcache(q4, kc, vc, k=k4, v=vv4, cache_seqlens=cs2, block_table=bt)
+    ref_app = A.paged_decode_attention(q, v2[0, 0], v2[0, 1], bt, cs2 + 1, 1 / math.sqrt(64), ms,
+                                       key=key, value=val)
+    torch.cuda.synchronize()
+    assert torch.equal(storage.view(torch.int16), two.view(torch.int16))
+    assert torch.equal(got.view(-1).view(torch.int16), ref_app.view(-1).view(torch.int16))
