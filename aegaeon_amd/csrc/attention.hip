@@ -74,6 +74,10 @@ constexpr int kMaxBatch = 2048;     // sequences per launch (LDS prefix sums); l
                                     // batches are launched in chunks
 constexpr int kMaxWorkgroups = 8192;  // bound of n_workgroups
 constexpr int kMaxStage = 4;          // finished pieces a wave stages in LDS
+constexpr int kNewStage = 8;          // an appending call: sequences' new rows a wave stages in LDS
+// A raw buffer offset past every range this file builds (each below 2^31
+// bytes): the access returns zeros and reads no memory.
+constexpr uint32_t kPastRange = 0xFFFFFFF0u;
 constexpr int kStageBudget = 64 * 1024;  // dynamic LDS of a workgroup, scan arrays included
 constexpr int kScanPerThread = kMaxBatch / (64 * kHeadsPerGroup);
 // Cost of switching the block stream to a new sequence (its piece staged,
@@ -181,6 +185,8 @@ struct AttnArgs {
   const uint16_t* knew;
   const uint16_t* vnew;
   int64_t knew_bstride, vnew_bstride;  // elements
+  uint32_t knew_span, vnew_span;       // bytes from knew / vnew to the last row's end (< 2^31)
+  int32_t newrow_off;                  // byte offset of the staged new rows in dynamic LDS
   int32_t n_desc;                      // merge descriptors (the combine grid's width)
 };
 
@@ -203,7 +209,8 @@ inline bool desc_per_sequence(int64_t batch, int64_t n_groups, int64_t n_wg) {
 // i - bcum[b] of the sequence b holding it), and their new-row tags (b * 16 +
 // the token offset of the last token in a sequence's last block, -1 for other
 // blocks and for sequences longer than max_seq_len), which an appending call
-// uses.
+// at D = 256 uses (at D <= 128 it finds each sequence's last block from the
+// stream's own position instead).
 struct PlanLayout {
   int64_t wg, desc, first, last, ids, tags, total;
 };
@@ -520,9 +527,12 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
                                              const int32_t* s_len, uint8_t* stage, int4* meta,
                                              int grp, int b0, int i0, int i1, bool have_first,
                                              int id_first, int tag_first,
-                                             const uint32_t* s_over = nullptr) {
+                                             const uint32_t* s_over = nullptr,
+                                             uint8_t* nstage = nullptr, int32_t* nseq = nullptr) {
   constexpr int KS = D / 32;
   constexpr int DPL = D / 16;
+  constexpr bool kNewInLds = FUSED && D <= 128;  // an appending call's rows staged in LDS
+  constexpr bool kTags = FUSED && !kNewInLds;     // per-item new-row tags (D = 256)
   const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
   const int h = grp * kHeadsPerGroup + wave;
   if (h >= a.n_kv_heads) return;  // wave past the last kv head (uniform)
@@ -547,17 +557,18 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   // block id of item i (clamped into the range), one lane per item; bh is a
   // sequence at or before the item's (the item's own or the next one are
   // checked before a search).  An appending call also takes the item's
-  // new-row tag: b * 16 + the offset of sequence b's new token when the item
+  // new-row tag (D = 256 only: its loads select the rows per lane): b * 16 +
+  // the offset of sequence b's new token when the item
   // is b's last block, else -1.
   auto item_id = [&](int i, int bh, int& tag) -> int {
     i = min(i, i1 - 1);
     if constexpr (PLANNED) {
-      if constexpr (FUSED) tag = a.plan_tags[i];
+      if constexpr (kTags) tag = a.plan_tags[i];
       return a.plan_ids[i];
     } else {
       int b = bh;
       if (s_bcum[b + 1] <= i) b = s_bcum[b + 2] > i ? b + 1 : seq_at(s_bcum, a.batch, i);
-      if constexpr (FUSED)  // the new row, unless it lies past the attended range
+      if constexpr (kTags)  // the new row, unless it lies past the attended range
         tag = i == s_bcum[b + 1] - 1 && !((s_over[b >> 5] >> (b & 31)) & 1u)
                   ? b * kBlockSize + ((s_len[b] - 1) & (kBlockSize - 1)) : -1;
       return a.block_tables[(int64_t)b * a.max_blocks + (i - s_bcum[b])];
@@ -576,7 +587,7 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
       cbase += 64;
       id_nxt = item_id(cbase + 64 + lane, bc, tag_nxt);
     }
-    if constexpr (FUSED) tag = __builtin_amdgcn_readlane(tag_cur, i - cbase);
+    if constexpr (kTags) tag = __builtin_amdgcn_readlane(tag_cur, i - cbase);
     const int id = __builtin_amdgcn_readlane(id_cur, i - cbase);
     return (id >= 0 && id < a.n_blocks) ? id : -1;
   };
@@ -597,26 +608,88 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
 
   u32x4 qv[KS];
   load_q(bc, qv);
-  // An appending call keeps the new token's K and V rows of the sequence
-  // being computed in registers (lane (j, g): K dims 8g + 32ks, V dims
-  // D/16 * j), loaded when the stream switches to the sequence, and patches
-  // them into the sequence's last block after its ordinary loads; D = 256,
-  // which has no registers to spare, selects the rows per lane at load time.
-  constexpr bool kNewInRegs = FUSED && D <= 128;
+  // An appending call (D <= 128) keeps the new token's K and V rows of the
+  // next kNewStage sequences of its stream in LDS, for this wave's kv head:
+  // kNewStage K rows, then as many V rows (`nstage`).  They are loaded when
+  // the stream starts (the loads issue right behind the first block's and are
+  // written to LDS once the pipeline's other first loads are issued, so that
+  // write waits for the first block and the rows only, and the compiler's
+  // waits count the pipeline's loads exactly), and again at a sequence switch that
+  // reaches past the staged sequences (a rare path that waits for every load
+  // in flight).  A sequence's last block is patched from LDS after its
+  // ordinary loads: no load of the block loop is conditional, so the loop's
+  // waits are those of the plain call.  (Keeping the rows of the sequence in
+  // registers, loaded at each switch, made the compiler wait for all but the
+  // newest block at every patch.)  D = 256 selects the rows per lane at load
+  // time instead.
   constexpr int VW = KVRegs<D>::VW;
-  u32x4 knr[kNewInRegs ? KS : 1];
-  uint32_t vnr[kNewInRegs ? VW : 1];
-  auto load_new = [&](int b) {
-    if constexpr (kNewInRegs) {
-      const uint16_t* kp = a.knew + (int64_t)b * a.knew_bstride + (int64_t)h * D + 8 * g;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        knr[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 32 * ks));
-      load_words_global<VW>(a.vnew + (int64_t)b * a.vnew_bstride + (int64_t)h * D + DPL * j,
-                            vnr);
+  constexpr int RB = 2 * D;            // bytes of one kv head's row
+  constexpr int EPI = 1024 / RB;       // rows per wave-wide 16-byte load
+  constexpr int NLD = kNewInLds ? kNewStage / EPI : 1;  // such loads per side
+  static_assert(!kNewInLds || kNewStage % EPI == 0, "whole loads of staged rows");
+  int e_stage = 0, n_staged = 0;  // bc's entry in the staged rows, entries staged
+  // the item of sequence bc whose block holds its new row (-1: none in range,
+  // or the sequence is longer than max_seq_len) and the row's offset in it
+  int patch_at = -1, patch_off = 0;
+  auto set_patch = [&]() {
+    if constexpr (kNewInLds) {
+      const bool over = (s_over[bc >> 5] >> (bc & 31)) & 1u;
+      patch_at = cend == uni(s_bcum[bc + 1]) && !over ? cend - 1 : -1;
+      patch_off = (len - 1) & (kBlockSize - 1);
     }
   };
-  load_new(bc);
+  set_patch();
+  // Entries [0, n) from sequence bs: the next n non-empty sequences among the
+  // 64 from bs, n <= kNewStage; nseq[k] = the sequence of entry k, or -1 when
+  // its new row is not attended here (its last block lies past the range, or
+  // it is longer than max_seq_len).  Returns n.
+  auto stage_seqs = [&](int bs) -> int {
+    const int b = bs + lane;
+    const bool ne = b < a.batch && s_bcum[b + 1] > s_bcum[b];
+    const uint64_t mask = __builtin_amdgcn_ballot_w64(ne);
+    const int rank = (int)__builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+    if (lane < kNewStage) nseq[lane] = -1;  // entries past n load nothing
+    if (ne && rank < kNewStage)
+      nseq[rank] = s_bcum[b + 1] <= i1 && !((s_over[b >> 5] >> (b & 31)) & 1u) ? b : -1;
+    return min(kNewStage, (int)__builtin_popcountll(mask));
+  };
+  // One 16-byte piece of a staged row per lane and load: load k holds rows
+  // k * EPI + lane / (RB / 16), bytes 16 * (lane % (RB / 16)) of each.  A
+  // row that is not needed reads through an offset past the buffer range
+  // (zeros, no memory access).
+  u32x4 nk[NLD], nv[NLD];
+  auto issue_new = [&]() {
+    if constexpr (kNewInLds) {
+      // the ranges are built where they are used (the compiler would otherwise
+      // keep them in scalar registers across the block loop)
+      const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.knew);
+      const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.vnew);
+      asm volatile("" : "+s"(kb), "+s"(vb));
+      const auto krs = byte_range(kb, a.knew_span);
+      const auto vrs = byte_range(vb, a.vnew_span);
+      const uint32_t off = (uint32_t)(h * RB + 16 * (lane % (RB / 16)));
+#pragma unroll
+      for (int k = 0; k < NLD; ++k) {
+        const int b = nseq[k * EPI + lane / (RB / 16)];
+        nk[k] = __builtin_amdgcn_raw_buffer_load_b128(
+            krs, b >= 0 ? (uint32_t)b * (uint32_t)(2 * a.knew_bstride) + off : kPastRange, 0,
+            kNt);
+        nv[k] = __builtin_amdgcn_raw_buffer_load_b128(
+            vrs, b >= 0 ? (uint32_t)b * (uint32_t)(2 * a.vnew_bstride) + off : kPastRange, 0,
+            kNt);
+      }
+    }
+  };
+  auto commit_new = [&]() {
+    if constexpr (kNewInLds) {
+#pragma unroll
+      for (int k = 0; k < NLD; ++k) {
+        *reinterpret_cast<u32x4*>(nstage + 1024 * k + 16 * lane) = nk[k];
+        *reinterpret_cast<u32x4*>(nstage + kNewStage * RB + 1024 * k + 16 * lane) = nv[k];
+      }
+    }
+  };
 
   f32x4 acc[DPL];
 #pragma unroll
@@ -644,15 +717,31 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
 
   int ic = i0;  // next item to compute
   auto compute = [&](KVRegs<D>& r, int id, int tag) {
-    if constexpr (kNewInRegs) {
-      if (tag >= 0) {  // the sequence's last block holds its new row (uniform)
-        const int noff = tag & (kBlockSize - 1);
+    if constexpr (kNewInLds) {
+      if (ic == patch_at) {  // the sequence's last block holds its new row (uniform)
+        const int noff = patch_off;
+        const uint8_t* kr = nstage + e_stage * RB;  // lane: dims 8g + 32ks
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) r.k[ks] = j == noff ? knr[ks] : r.k[ks];
+        for (int ks = 0; ks < KS; ++ks) {
+          const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + 2 * (8 * g + 32 * ks));
+          r.k[ks] = j == noff ? kk : r.k[ks];
+        }
+        uint32_t vw[VW];  // lane: dims D/16 * j
+        const uint8_t* vp = kr + kNewStage * RB + 2 * DPL * j;
+        if constexpr (VW == 2) {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
+          vw[0] = x.x; vw[1] = x.y;
+        } else {
+#pragma unroll
+          for (int i = 0; i < VW / 4; ++i) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(vp + 16 * i);
+            vw[4 * i] = x.x; vw[4 * i + 1] = x.y; vw[4 * i + 2] = x.z; vw[4 * i + 3] = x.w;
+          }
+        }
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int w = 0; w < VW; ++w) r.v[c][w] = 4 * g + c == noff ? vnr[w] : r.v[c][w];
+          for (int w = 0; w < VW; ++w) r.v[c][w] = 4 * g + c == noff ? vw[w] : r.v[c][w];
       }
     }
     compute_block<DT, D>(r, qv, acc, m, lsum, (ic - first) * kBlockSize, id >= 0 ? len : 0, g,
@@ -676,7 +765,15 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
         len = uni(s_len[bc]);
         complete = cend == uni(s_bcum[bc + 1]);  // it starts in range
         load_q(bc, qv);
-        load_new(bc);
+        set_patch();
+        if constexpr (kNewInLds) {
+          if (++e_stage == n_staged) {  // past the staged sequences (rare): stage the next
+            e_stage = 0;
+            n_staged = stage_seqs(bc);
+            issue_new();
+            commit_new();
+          }
+        }
 #pragma unroll
         for (int t = 0; t < DPL; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         m = -INFINITY;
@@ -697,7 +794,7 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
   const uint16_t* vn_lane = FUSED ? a.vnew + (int64_t)h * D + DPL * j : nullptr;
   auto load_item = [&](KVRegs<D>& r, int id, int tag, bool valid) {
     const int64_t off = (int64_t)max(id, 0) * a.blk_stride;
-    if constexpr (FUSED && !kNewInRegs) {
+    if constexpr (FUSED && !kNewInLds) {
       const int b = tag >> 4, noff = tag < 0 ? -1 : (tag & (kBlockSize - 1));
       load_block_new<D>(r, kh, vh, off, row, noff, kn_lane + (int64_t)b * a.knew_bstride,
                         vn_lane + (int64_t)b * a.vnew_bstride);
@@ -718,8 +815,13 @@ __device__ __forceinline__ void attend_items(const AttnArgs& a, const int32_t* s
     tags[k] = -1;
     ids[k] = id_at(min(i0 + k, i1 - 1), tags[k]);
     load_item(buf[k], ids[k], tags[k], i0 + k < i1);
+    if constexpr (kNewInLds && k == 0) {  // behind the first block's loads
+      n_staged = stage_seqs(bc);
+      issue_new();
+    }
     return false;
   });
+  commit_new();  // waits for the first block and the staged rows only
   for (int it = 0; it < nfull; it += NBUF) {
     unrolled_steps<NBUF>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
@@ -838,6 +940,7 @@ paged_decode_attention_kernel(AttnArgs a) {
   __shared__ int32_t s_find[2];
   __shared__ int4 s_meta[kHeadsPerGroup][kMaxStage];
   __shared__ uint32_t s_over[FUSED ? kMaxBatch / 32 : 1];
+  __shared__ int32_t s_newseq[kHeadsPerGroup][FUSED ? kNewStage : 1];
   int32_t* s_cum = s_mem;
   int32_t* s_len = s_mem + a.batch + 1;
   int32_t* s_bcum = s_len + a.batch;
@@ -852,10 +955,11 @@ paged_decode_attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < kPlanRecord; ++k) rec[k] = a.plan_wg[(int64_t)blockIdx.x * kPlanRecord + k];
     id_first = a.plan_first[(int64_t)blockIdx.x * 128 + lane];
-    if constexpr (FUSED) tag_first = a.plan_first[(int64_t)blockIdx.x * 128 + 64 + lane];
+    if constexpr (FUSED && D > 128)  // per-item tags: the lane-select path only
+      tag_first = a.plan_first[(int64_t)blockIdx.x * 128 + 64 + lane];
   }
   scan_batch(a.seq_lens, a.batch, a.max_seq_len, s_cum, s_bcum, s_len, s_wave_tot,
-             FUSED && !PLANNED ? s_over : nullptr);
+             FUSED ? s_over : nullptr);
   // Empty sequences have no positions: workgroup b % n_wg writes their zeros.
   for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
     if (s_cum[b + 1] != s_cum[b]) continue;  // uniform over the workgroup
@@ -866,6 +970,7 @@ paged_decode_attention_kernel(AttnArgs a) {
 
   uint8_t* stage = reinterpret_cast<uint8_t*>(s_mem) + a.stage_off +
                    wave * a.stage_slots * a.group * 4 * stage_record_bytes<D>();
+  uint8_t* nstage = reinterpret_cast<uint8_t*>(s_mem) + a.newrow_off + wave * kNewStage * 4 * D;
   if constexpr (PLANNED) {
     if (uni(rec[0]) < 0) return;  // idle workgroup
     const int items = s_bcum[a.batch];
@@ -877,7 +982,8 @@ paged_decode_attention_kernel(AttnArgs a) {
       if (i1 > i0)
         attend_items<DT, D, NBUF, true, FUSED>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0,
                                                i0, i1, first_pass, id_first,
-                                               first_pass ? tag_first : -1);
+                                               first_pass ? tag_first : -1, s_over, nstage,
+                                               s_newseq[wave]);
     }
     return;
   }
@@ -930,7 +1036,8 @@ paged_decode_attention_kernel(AttnArgs a) {
     }
     if (i1 > i0)
       attend_items<DT, D, NBUF, false, FUSED>(a, s_bcum, s_len, stage, s_meta[wave], grp, b0,
-                                              i0, i1, false, 0, -1, s_over);
+                                              i0, i1, false, 0, -1, s_over, nstage,
+                                              s_newseq[wave]);
     P = q_end;
     __syncthreads();  // s_find is rewritten by the next pass
   }
@@ -1082,45 +1189,52 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup) void decode_plan_kernel(PlanAr
 // keeps PB = 12 at ~110 VGPRs (PB = 16 measured 1 us slower on the
 // Yi-1.5-9B batch, whose longest sequences have 10-15 pieces; 8 the same).
 // The cache write of an appending call, spread over every thread of the
-// combine grid after its merges (extra grid rows for it measured 0.25 us per
-// Qwen2.5-7B layer): the new token's K and V rows of every sequence and kv
-// head go to token (len - 1) % 16 of the sequence's last block, 16 bytes per
-// lane.  The main kernel read those rows from the append's input, so nothing
-// reads the slot before this write.  Blocks outside the pool are skipped, as
-// the attention masks them.
+// combine grid (extra grid rows for it measured 0.25 us per Qwen2.5-7B
+// layer): the new token's K and V rows of every sequence and kv head go to
+// token (len - 1) % 16 of the sequence's last block, 16 bytes per lane.  The
+// main kernel read those rows from the append's input, so nothing reads the
+// slot before this write.  Blocks outside the pool are skipped, as the
+// attention masks them.  A thread's first chunk is loaded, with its length
+// and (planned) block id, before the workgroup's merge and stored after it,
+// so the merge does not wait behind the copy's round trip; further chunks
+// (batches whose rows outnumber the grid's threads) are copied after it.
 template <int D>
-__device__ __forceinline__ void copy_new_rows(const AttnArgs& a) {
-  constexpr int C = D / 8;  // 16-byte chunks of one kv head's row
-  const int64_t total = (int64_t)a.batch * a.n_kv_heads * 2 * C;
-  const int64_t stride = (int64_t)gridDim.x * gridDim.y * blockDim.x;
-  const int64_t row = (int64_t)a.n_kv_heads * D;
-  for (int64_t c = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
-       c < total; c += stride) {
-    const int chunk = (int)(c % C);
+struct NewRowChunk {
+  int b, kv, h, chunk;
+  __device__ NewRowChunk(const AttnArgs& a, int64_t c) {
+    constexpr int C = D / 8;  // 16-byte chunks of one kv head's row
+    chunk = (int)(c % C);
     const int64_t rest = c / C;
-    const int kv = (int)(rest & 1);
-    const int h = (int)((rest >> 1) % a.n_kv_heads);
-    const int b = (int)((rest >> 1) / a.n_kv_heads);
-    // the new row goes to its own position len - 1 (the append's slot), also
-    // when the length exceeds the attended bound; a table without a block
-    // for it gets nothing, as the append skips a slot outside the pool
-    const int len = a.seq_lens[b];
-    if (len <= 0) continue;
-    int blk;
-    if (a.plan_last) {
-      blk = a.plan_last[b];
-    } else {
-      if ((len - 1) / kBlockSize >= a.max_blocks) continue;
+    kv = (int)(rest & 1);
+    h = (int)((rest >> 1) % a.n_kv_heads);
+    b = (int)((rest >> 1) / a.n_kv_heads);
+  }
+  __device__ const u32x4* src(const AttnArgs& a) const {
+    return reinterpret_cast<const u32x4*>(
+        (kv ? a.vnew + (int64_t)b * a.vnew_bstride : a.knew + (int64_t)b * a.knew_bstride) +
+        (int64_t)h * D + 8 * chunk);
+  }
+  // the new row goes to its own position len - 1 (the append's slot), also
+  // when the length exceeds the attended bound; a table without a block for
+  // it gets nothing, as the append skips a slot outside the pool.  `blk`: the
+  // plan's block of that position when planned (loaded by the caller).
+  __device__ u32x4* dst(const AttnArgs& a, int len, int blk) const {
+    if (len <= 0) return nullptr;
+    if (!a.plan_last) {
+      if ((len - 1) / kBlockSize >= a.max_blocks) return nullptr;
       blk = a.block_tables[(int64_t)b * a.max_blocks + (len - 1) / kBlockSize];
     }
-    if (blk < 0 || blk >= a.n_blocks) continue;
-    const uint16_t* src = (kv ? a.vnew + (int64_t)b * a.vnew_bstride
-                              : a.knew + (int64_t)b * a.knew_bstride) + (int64_t)h * D + 8 * chunk;
-    uint16_t* dst = const_cast<uint16_t*>(kv ? a.vc : a.kc) + (int64_t)blk * a.blk_stride +
-                    (int64_t)((len - 1) % kBlockSize) * row + (int64_t)h * D + 8 * chunk;
-    __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src)),
-                                reinterpret_cast<u32x4*>(dst));
+    if (blk < 0 || blk >= a.n_blocks) return nullptr;
+    const int64_t row = (int64_t)a.n_kv_heads * D;
+    return reinterpret_cast<u32x4*>(const_cast<uint16_t*>(kv ? a.vc : a.kc) +
+                                    (int64_t)blk * a.blk_stride +
+                                    (int64_t)((len - 1) % kBlockSize) * row + (int64_t)h * D +
+                                    8 * chunk);
   }
+};
+template <int D>
+__device__ __forceinline__ int64_t new_row_chunks(const AttnArgs& a) {
+  return (int64_t)a.batch * a.n_kv_heads * 2 * (D / 8);
 }
 
 
@@ -1194,20 +1308,45 @@ __device__ __forceinline__ void merge_pieces(const AttnArgs& a, const int4 d) {
 template <int DT, int D, int KI, int PB>
 __global__ __launch_bounds__(64 * kHeadsPerGroup) void attention_combine_kernel(AttnArgs a) {
   const int4 d = a.desc[blockIdx.x];
+  // an appending call: this thread's first new-row chunk, loaded ahead of the merge
+  const int64_t total = a.knew ? new_row_chunks<D>(a) : 0;
+  const int64_t stride = (int64_t)gridDim.x * gridDim.y * blockDim.x;
+  const int64_t c0 = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
+  u32x4 v0 = {0u, 0u, 0u, 0u};
+  int len0 = 0, blk0 = -1;
+  if (c0 < total) {
+    const NewRowChunk<D> r(a, c0);
+    v0 = __builtin_nontemporal_load(r.src(a));
+    len0 = a.seq_lens[r.b];
+    if (a.plan_last) blk0 = a.plan_last[r.b];
+  }
   if (d.x >= 0) merge_pieces<DT, D, KI, PB>(a, d);  // uniform over the workgroup
-  if (a.knew) copy_new_rows<D>(a);  // an appending call: the new rows, spread over the grid
+  if (c0 < total) {
+    const NewRowChunk<D> r(a, c0);
+    if (u32x4* p = r.dst(a, len0, blk0)) __builtin_nontemporal_store(v0, p);
+  }
+  for (int64_t c = c0 + stride; c < total; c += stride) {
+    const NewRowChunk<D> r(a, c);
+    if (u32x4* p = r.dst(a, a.seq_lens[r.b], a.plan_last ? a.plan_last[r.b] : -1))
+      __builtin_nontemporal_store(__builtin_nontemporal_load(r.src(a)), p);
+  }
 }
 
 // Dynamic LDS of the main kernel: the scan arrays, then (16-byte aligned) the
-// staging records of the four waves.  Sets a.stage_slots and a.stage_off.
+// staging records of the four waves, then an appending call's staged new rows
+// (D <= 128: kNewStage K and V rows per wave).  Sets a.stage_slots,
+// a.stage_off and a.newrow_off.
 size_t lds_bytes(AttnArgs& a, int max_lds) {
   const int64_t scan = ((int64_t)(3 * a.batch + 2) * (int64_t)sizeof(int32_t) + 15) / 16 * 16;
   const int64_t per_slot = (int64_t)kHeadsPerGroup * a.group * 4 * (a.head_dim + 16);
-  const int64_t budget = std::min<int64_t>(kStageBudget, max_lds) - scan;
+  const int64_t newrows =
+      a.knew && a.head_dim <= 128 ? (int64_t)kHeadsPerGroup * kNewStage * 4 * a.head_dim : 0;
+  const int64_t budget = std::min<int64_t>(kStageBudget, max_lds - newrows) - scan;
   a.stage_off = (int32_t)scan;
   a.stage_slots = a.head_dim > 128 ? 0
                   : (int32_t)std::max<int64_t>(0, std::min<int64_t>(kMaxStage, budget / per_slot));
-  return (size_t)(scan + a.stage_slots * per_slot);
+  a.newrow_off = (int32_t)(scan + a.stage_slots * per_slot);
+  return (size_t)(a.newrow_off + newrows);
 }
 
 // Workgroups of the main kernel for one launch: one per CU (measured on the
@@ -1350,6 +1489,7 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
   a.vnew = static_cast<const uint16_t*>(nr.value);
   a.knew_bstride = nr.key_bstride;
   a.vnew_bstride = nr.value_bstride;
+  a.knew_span = a.vnew_span = 0;
   a.n_desc = n_wg;
   if (plan) {
     if (desc_per_sequence(batch, n_groups, n_wg)) a.n_desc = batch * n_groups;
@@ -1385,6 +1525,13 @@ int run_attention(void* out, int64_t out_batch_stride, const void* q, int64_t q_
     if (nr.key) {
       a.knew = static_cast<const uint16_t*>(nr.key) + (int64_t)c * nr.key_bstride;
       a.vnew = static_cast<const uint16_t*>(nr.value) + (int64_t)c * nr.value_bstride;
+      // the staged rows' buffer ranges: row b of kv head h at b * stride + h * D
+      const int64_t row_end = (int64_t)n_kv_heads * head_dim * 2;
+      const int64_t ks = (int64_t)(a.batch - 1) * nr.key_bstride * 2 + row_end;
+      const int64_t vs = (int64_t)(a.batch - 1) * nr.value_bstride * 2 + row_end;
+      if (ks >= (1ll << 31) || vs >= (1ll << 31)) return AEGKV_ERR_UNSUPPORTED;
+      a.knew_span = (uint32_t)ks;
+      a.vnew_span = (uint32_t)vs;
     }
     const size_t lds = lds_bytes(a, ds->max_lds);
     switch (head_dim) {

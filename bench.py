@@ -274,10 +274,10 @@ def bench_attention(args, timer, wb=None, label="Qwen2.5-7B"):
         raise RuntimeError("fused and two-launch append + attention disagree")
     del unplanned_out, two_out
     steps = max(g.n_layers, (args.steps // g.n_layers) * g.n_layers)
-    # the four forms alternate over three rounds and each keeps its best round,
+    # the five forms alternate over seven rounds and each keeps its best round,
     # so that a slow stretch of the box does not fall on one form only
     best = {}
-    for _ in range(3):
+    for _ in range(7):
         for name, fn in (("unplanned", layer_call), ("planned", planned_call),
                          ("kvcache", kvcache_call), ("two", two_launch_call),
                          ("fused", fused_call)):
