@@ -91,9 +91,9 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(AppendArgs a)
 // Measured and dropped: two tiles in flight per workgroup, with the ids two
 // tiles ahead, 5.0-5.5 TB/s over 8-64 workgroups per CU; a tile order that
 // puts a block's K and V passes side by side (32 KiB adjacent reads),
-// 5.3-5.5 TB/s.  The same 16 KiB units moved by the block-copy kernel run at
-// 5.0-5.2 TB/s, a contiguous copy of the same bytes at 6.2 TB/s: the
-// scattered 16 KiB sources are the bound.)
+// 5.3-5.5 TB/s.  The same 16 KiB units moved by the block-copy kernel (one
+// wave per 1 KiB) run at 5.52-5.54 TB/s, a contiguous copy of the same bytes
+// at 6.3 TB/s: the scattered 16 KiB sources are the bound.)
 constexpr int kGatherThreads = 256;
 constexpr int kGatherMaxBatch = 1024;  // sequences per launch (LDS scan)
 constexpr int kGatherWorkgroupsPerCu = 64;  // 8..256 measured: 64 best, 128 10% and 256 40% slower

@@ -3,21 +3,29 @@
 // (aegaeon/ops/swap.cu:25-59).
 //
 // One kernel serves every device-side move.  A block of block_bytes is cut into
-// tiles of 8 KiB and the tiles of all blocks are laid end to end; one
-// short-lived workgroup copies one tile (a grid of at most kMaxCopyGrid
-// workgroups loops over the rest).  A workgroup reads its block's source and
-// destination ids with scalar loads, then each lane issues its kTileUnroll
-// non-temporal dwordx4 loads before its stores (every access a fully coalesced
-// 1 KiB wave row).  Loads and stores are raw buffer instructions bounded to
-// the tile's valid bytes (no exec branches around memory), which keeps the
-// compiler's wait counts exact.
+// 1 KiB tiles; one short-lived workgroup of a single wave copies one tile, on
+// a two-dimensional grid (y: the block, x: its tile; a block of more tiles
+// than one grid row holds loops its row, more blocks than one launch holds
+// take several launches), so no workgroup divides to find its block.  The
+// wave reads its block's source and destination ids with scalar loads (the
+// same ids for every tile of a block, so they hit the scalar cache), then
+// each lane issues one non-temporal dwordx4 load and one store: the tile is
+// one fully coalesced 1 KiB wave row each way.  Loads and stores are raw
+// buffer instructions bounded to the tile's valid bytes (no exec branches
+// around memory), which keeps the compiler's wait counts exact.
 //
-// Measured on MI355X (same process, 1024 x 12.5 MiB pool, 256 scattered blocks
-// packed, 6.4 GB moved): 8 KiB tiles one per workgroup 6.08 TB/s, 16 KiB 6.01,
-// 32 KiB 5.49, against 5.33 TB/s for the earlier persistent grid (32
-// workgroups per CU walking 16 KiB tiles with the next tile's ids prefetched);
-// a contiguous 1 GiB copy: 16 KiB per workgroup 6.30 TB/s, 8 KiB 6.07, the
-// persistent grid 6.05, hipMemcpyAsync 5.13.
+// Measured on MI355X (bench sections, two rounds each, TB/s for the
+// Llama-2-13B pack / scatter of 4096 x 12.5 MiB blocks, the unified-pool
+// defrag, and a contiguous copy of the pack's 107 GB): one wave per 1 KiB
+// tile 6.39-6.44 / 6.81 / 6.64 / 6.50-6.61; 64 lanes x 2 KiB 5.85-5.90 /
+// 6.44-6.47 / 5.99-6.01; 64 x 4 KiB 5.99-6.04 / 6.51-6.57 / 5.70-5.83;
+// 256 lanes x 4 KiB 6.25-6.31 / 6.52-6.56 / 6.13-6.16; 256 x 8 KiB (the
+// earlier tile, with a 64-bit division per workgroup) 5.97-6.05 /
+// 6.58-6.63 / 5.75-5.89 / 5.80-6.02 (16 KiB contiguous tiles); 512 x 8 KiB
+// 6.14-6.25 / 6.63-6.72 / 6.20-6.26 / 6.10-6.59.  Many one-wave workgroups
+// with one load and one store per lane keep the most bytes in flight; the
+// earlier persistent grid (32 workgroups per CU walking 16 KiB tiles) ran at
+// 5.33 TB/s, hipMemcpyAsync of a contiguous 1 GiB at 5.13.
 #include <algorithm>
 #include <cstring>
 #include <numeric>
@@ -26,7 +34,7 @@
 #include "aegkv_internal.h"
 
 #ifndef AEGKV_TILE_UNROLL
-#define AEGKV_TILE_UNROLL 2
+#define AEGKV_TILE_UNROLL 1
 #endif
 
 namespace aegkv {
@@ -34,15 +42,24 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kCopyThreads = 256;
-constexpr int kTileUnroll = AEGKV_TILE_UNROLL;  // dwordx4 per lane per tile: 8 KiB tiles
-// Identity copies (no id list on either side) move contiguous bytes: 16 KiB
-// per workgroup measured best there.
-constexpr int kLinearUnroll = 4;
+#ifndef AEGKV_COPY_THREADS
+#define AEGKV_COPY_THREADS 64
+#endif
+constexpr int kCopyThreads = AEGKV_COPY_THREADS;
+constexpr int kTileUnroll = AEGKV_TILE_UNROLL;  // dwordx4 per lane per tile: 1 KiB tiles
+// Identity copies (no id list on either side) move one contiguous range:
+// 1 KiB tiles measured best there too (107 GB: 6.50-6.61 TB/s against
+// 6.07-6.32 for 4 KiB and 5.70-5.73 for 8 KiB; the 29.4 MB copy floor the
+// same within 0.1 us).
+#ifndef AEGKV_LINEAR_UNROLL
+#define AEGKV_LINEAR_UNROLL 1
+#endif
+constexpr int kLinearUnroll = AEGKV_LINEAR_UNROLL;
 // Largest grid of one launch: HIP bounds a launch to 2^32 - 1 work-items per
-// dimension; beyond this many tiles the kernel's loop deals the rest to the
-// same workgroups.
-constexpr uint64_t kMaxCopyGrid = 1ull << 23;
+// dimension; a block of more tiles loops its grid row over the rest, and more
+// than kMaxCopyGridY blocks take several launches.
+constexpr uint64_t kMaxCopyGrid = (1ull << 31) / kCopyThreads;
+constexpr int64_t kMaxCopyGridY = 65535;
 static_assert(kMaxCopyGrid * kCopyThreads <= 0xFFFFFFFFull,
               "the copy grid must fit one launch dimension");
 
@@ -54,16 +71,19 @@ template <bool SRC_IDS, bool DST_IDS, int UNROLL>
 __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
     const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
     const int64_t* __restrict__ src_ids, const int64_t* __restrict__ dst_ids,
-    uint64_t block_bytes, uint32_t tiles_per_block, uint64_t n_tiles) {
-  constexpr uint64_t TILE = (uint64_t)kCopyThreads * 16 * UNROLL;
-  for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-    const uint64_t i = tile / tiles_per_block;  // block index of the tile
-    const int64_t s = SRC_IDS ? src_ids[i] : (int64_t)i;
-    const int64_t d = DST_IDS ? dst_ids[i] : (int64_t)i;
-    const uint64_t base = (tile - i * tiles_per_block) * TILE;
-    const uint32_t bytes = (uint32_t)min(block_bytes - base, TILE);
-    const auto sr = byte_range(src + (uint64_t)s * block_bytes + base, bytes);
-    const auto dr = byte_range(dst + (uint64_t)d * block_bytes + base, bytes);
+    uint64_t block_bytes, uint32_t tiles_per_block) {
+  constexpr uint32_t TILE = (uint32_t)kCopyThreads * 16 * UNROLL;
+  // grid y: the block (of this launch's chunk), grid x: its tile; no division
+  const int64_t i = blockIdx.y;
+  const int64_t s = SRC_IDS ? src_ids[i] : i;
+  const int64_t d = DST_IDS ? dst_ids[i] : i;
+  const uint8_t* sb = src + (uint64_t)s * block_bytes;
+  uint8_t* db = dst + (uint64_t)d * block_bytes;
+  for (uint32_t t = blockIdx.x; t < tiles_per_block; t += gridDim.x) {
+    const uint64_t base = (uint64_t)t * TILE;
+    const uint32_t bytes = (uint32_t)min(block_bytes - base, (uint64_t)TILE);
+    const auto sr = byte_range(sb + base, bytes);
+    const auto dr = byte_range(db + base, bytes);
     u32x4 r[UNROLL];
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k)
@@ -76,19 +96,24 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
   }
 }
 
+// Blocks [0, n) in launches of at most kMaxCopyGridY blocks (grid y), each
+// block's tiles along grid x (at most kMaxCopyGrid; a longer block loops).
 template <bool SRC_IDS, bool DST_IDS, int UNROLL>
 int launch_tiles(const void* src, void* dst, const int64_t* src_ids, const int64_t* dst_ids,
                  int64_t n, uint64_t block_bytes, hipStream_t stream) {
   constexpr uint64_t TILE = (uint64_t)kCopyThreads * 16 * UNROLL;
   const uint64_t tiles_per_block = (block_bytes + TILE - 1) / TILE;
   if (tiles_per_block > 0xFFFFFFFFull) return AEGKV_ERR_UNSUPPORTED;
-  const uint64_t n_tiles = tiles_per_block * (uint64_t)n;
-  const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, kMaxCopyGrid);
-  hipLaunchKernelGGL((copy_blocks_kernel<SRC_IDS, DST_IDS, UNROLL>), dim3(grid),
-                     dim3(kCopyThreads), 0, stream, static_cast<const uint8_t*>(src),
-                     static_cast<uint8_t*>(dst), src_ids, dst_ids, block_bytes,
-                     (uint32_t)tiles_per_block, n_tiles);
-  AEGKV_HIP_TRY(hipGetLastError());
+  const uint32_t gx = (uint32_t)std::min<uint64_t>(tiles_per_block, kMaxCopyGrid);
+  for (int64_t c0 = 0; c0 < n; c0 += kMaxCopyGridY) {
+    const uint32_t gy = (uint32_t)std::min<int64_t>(n - c0, kMaxCopyGridY);
+    const uint8_t* s = static_cast<const uint8_t*>(src) + (SRC_IDS ? 0 : c0 * block_bytes);
+    uint8_t* d = static_cast<uint8_t*>(dst) + (DST_IDS ? 0 : c0 * block_bytes);
+    hipLaunchKernelGGL((copy_blocks_kernel<SRC_IDS, DST_IDS, UNROLL>), dim3(gx, gy),
+                       dim3(kCopyThreads), 0, stream, s, d, SRC_IDS ? src_ids + c0 : nullptr,
+                       DST_IDS ? dst_ids + c0 : nullptr, block_bytes, (uint32_t)tiles_per_block);
+    AEGKV_HIP_TRY(hipGetLastError());
+  }
   return AEGKV_OK;
 }
 
@@ -109,7 +134,7 @@ int launch_copy_blocks(const DeviceState* ds, const void* src, void* dst,
     return launch_tiles<false, true, kTileUnroll>(src, dst, nullptr, dst_ids_dev, n,
                                                    block_bytes, stream);
   // identity: one contiguous range of n * block_bytes bytes, copied as a
-  // single block of 16 KiB tiles
+  // single block
   return launch_tiles<false, false, kLinearUnroll>(src, dst, nullptr, nullptr, 1,
                                                    (uint64_t)n * block_bytes, stream);
 }

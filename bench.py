@@ -1345,8 +1345,8 @@ def main(argv=None):
         f = res["floor"]
         fg = f["bytes"] / (f["ms"] * 1e-3) / 1e9
         ops_out["copy_floor_at_append_bytes"] = {
-            "workload": "the library's contiguous copy (copy_blocks without id lists: 16 KiB "
-                        "per workgroup), 14 contiguous 1 MiB blocks (29,360,128 B moved, the "
+            "workload": "the library's contiguous copy (copy_blocks without id lists: 1 KiB "
+                        "per one-wave workgroup), 14 contiguous 1 MiB blocks (29,360,128 B moved, the "
                         "headline append's bytes less its slots), 32 rotated regions",
             "us": round(f["ms"] * 1e3, 2), "bytes": f["bytes"], "GB/s": round(fg, 1),
             "frac_hbm": round(fg / HBM_PEAK_GBS, 4)}
