@@ -87,6 +87,51 @@ def test_pack_scatter_copy(device, block_bytes):
     assert np.array_equal(third.cpu().numpy(), ref3)
 
 
+def test_more_blocks_than_one_launch(device):
+    """70,000 blocks of 16 and of 1040 bytes (a full and a partial 1 KiB tile):
+    the copy kernel's grid holds at most 65,535 blocks, so the host issues
+    several launches with offset id lists and offset identity sides; pack,
+    scatter and the two-list copy against the oracle."""
+    for bb in (16, 1040):
+        rng = np.random.default_rng(bb + 70000)
+        N, n = 150000, 70000
+        pool_np = rng.integers(0, 256, size=(N, bb), dtype=np.uint8)
+        pool = torch.from_numpy(pool_np).to(device)
+        ids = rng.permutation(N)[:n]
+        staged = ops.pack_blocks(pool, ids)
+        want = ko.pack_blocks(pool_np, ids)
+        assert np.array_equal(staged.cpu().numpy(), want)
+        dst_ids = rng.permutation(N)[:n]
+        other = torch.zeros_like(pool)
+        ops.scatter_blocks(staged, dst_ids, other)
+        ref = np.zeros_like(pool_np)
+        ko.scatter_blocks(want, dst_ids, ref)
+        assert np.array_equal(other.cpu().numpy(), ref)
+        third = torch.zeros_like(pool)
+        ops.copy_blocks(pool, third, ids, dst_ids)
+        assert np.array_equal(third.cpu().numpy(), ref)
+
+
+def test_contiguous_copy_past_one_grid_row(device):
+    """An identity copy of 32 GiB + 1 MiB: more 1 KiB tiles (33,555,456) than one
+    grid row holds (2^31 work-items / 64 = 33,554,432), so the row's workgroups
+    loop over the rest.  Checked on the GPU: every byte, by comparing the two
+    buffers, after filling the source with random words."""
+    free, _ = torch.cuda.mem_get_info(device)
+    nbytes = (32 << 30) + (1 << 20)
+    if free < 2 * nbytes + (4 << 30):
+        pytest.skip("needs 68 GB of free device memory")
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device=device)
+    src.random_()
+    dst = torch.zeros_like(src)
+    ops.copy_blocks(src.view(torch.uint8).view(1, nbytes), dst.view(torch.uint8).view(1, nbytes),
+                    None, None)
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("block_bytes", [16400, 917504])
 def test_copy_without_id_lists(device, block_bytes):
     """aegkv_copy_blocks with both id lists null copies blocks 0..n-1 of one pool
