@@ -47,6 +47,13 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #endif
 constexpr int kCopyThreads = AEGKV_COPY_THREADS;
 constexpr int kTileUnroll = AEGKV_TILE_UNROLL;  // dwordx4 per lane per tile: 1 KiB tiles
+// Stores: non-temporal with device scope (nt sc1).  Bench sections, same call,
+// two rounds, TB/s against nt alone: pack 6.51-6.52 / 6.38-6.48, scatter
+// 6.83-6.85 / 6.78-6.79, defrag 6.71-6.72 / 6.60, copy calibration 6.11 /
+// 5.88-5.94; stores with no policy bits were slower (pack 6.22), and loads
+// with sc0 changed nothing.  A tile of a block of whole 1 KiB tiles is eight
+// whole 128-byte lines, so these stores write lines, not pieces of them.
+constexpr int kStorePolicy = kNt | 16;
 // Identity copies (no id list on either side) move one contiguous range:
 // 1 KiB tiles measured best there too (107 GB: 6.50-6.61 TB/s against
 // 6.07-6.32 for 4 KiB and 5.70-5.73 for 8 KiB; the 29.4 MB copy floor the
@@ -92,7 +99,7 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
 #pragma unroll
     for (int k = 0; k < UNROLL; ++k)
       __builtin_amdgcn_raw_buffer_store_b128(r[k], dr, (k * kCopyThreads + threadIdx.x) * 16, 0,
-                                             kNt);
+                                             kStorePolicy);
   }
 }
 
