@@ -25,10 +25,11 @@ inline bool aligned16(const void* p) {
 
 // Host-side validation of an id list against a pool of n_pool blocks.
 int check_ids_in_range(const int64_t* ids, int64_t n, uint64_t n_pool);
-// AEGKV_ERR_DUPLICATE if any id appears twice.
-int check_unique(const int64_t* ids, int64_t n);
-// AEGKV_ERR_OVERLAP if the two id sets intersect.
-int check_disjoint(const int64_t* a, int64_t na, const int64_t* b, int64_t nb);
+// AEGKV_ERR_DUPLICATE if any id appears twice (ids already checked to lie in
+// [0, n_pool)).
+int check_unique(const int64_t* ids, int64_t n, uint64_t n_pool);
+// AEGKV_ERR_OVERLAP if the two id sets intersect (ids in [0, n_pool)).
+int check_disjoint(const int64_t* a, int64_t na, const int64_t* b, int64_t nb, uint64_t n_pool);
 
 // Per-device state: compute-unit count and the id upload ring.  Host id lists
 // are copied into a pinned host slice and DMA'd to the matching device slice on

@@ -171,7 +171,7 @@ int copy_blocks_checked(const void* src_pool, uint64_t n_src_blocks, void* dst_p
   }
   if (dst_ids) {
     if ((rc = check_ids_in_range(dst_ids, n, n_dst_blocks))) return rc;
-    if ((rc = check_unique(dst_ids, n))) return rc;
+    if ((rc = check_unique(dst_ids, n, n_dst_blocks))) return rc;
   } else if ((uint64_t)n > n_dst_blocks) {
     return AEGKV_ERR_OUT_OF_RANGE;
   }
@@ -182,7 +182,8 @@ int copy_blocks_checked(const void* src_pool, uint64_t n_src_blocks, void* dst_p
     std::vector<int64_t> s, d;
     if (!src_ids) { s.resize(n); std::iota(s.begin(), s.end(), 0); }
     if (!dst_ids) { d.resize(n); std::iota(d.begin(), d.end(), 0); }
-    if ((rc = check_disjoint(src_ids ? src_ids : s.data(), n, dst_ids ? dst_ids : d.data(), n)))
+    if ((rc = check_disjoint(src_ids ? src_ids : s.data(), n, dst_ids ? dst_ids : d.data(), n,
+                             std::max(n_src_blocks, n_dst_blocks))))
       return rc;
   } else if (ranges_overlap(src_pool, n_src_blocks * block_bytes, dst_pool,
                             n_dst_blocks * block_bytes)) {
@@ -263,7 +264,7 @@ int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
   int rc;
   if ((rc = check_ids_in_range(src_ids, n, n_src))) return rc;
   if ((rc = check_ids_in_range(dst_ids, n, n_dst))) return rc;
-  if ((rc = check_unique(dst_ids, n))) return rc;
+  if ((rc = check_unique(dst_ids, n, n_dst))) return rc;
 
   uint8_t* dev = static_cast<uint8_t*>(dev_pool);
   uint8_t* host = static_cast<uint8_t*>(host_pool);
@@ -410,7 +411,7 @@ int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, in
   int rc;
   if ((rc = check_ids_in_range(src_ids, n, n_src))) return rc;
   if ((rc = check_ids_in_range(dst_ids, n, n_dst))) return rc;
-  if ((rc = check_unique(dst_ids, n))) return rc;
+  if ((rc = check_unique(dst_ids, n, n_dst))) return rc;
   const uint64_t bb = block_bytes;
   if ((bb & 15) || !aligned16(dev_pool) || !aligned16(staging)) return AEGKV_ERR_MISALIGNED;
   const uint64_t cap64 = std::min(staging_bytes, bounce_bytes) / bb;

@@ -15,7 +15,38 @@ int check_ids_in_range(const int64_t* ids, int64_t n, uint64_t n_pool) {
   return AEGKV_OK;
 }
 
-int check_unique(const int64_t* ids, int64_t n) {
+namespace {
+// Pools of up to 2^27 blocks are checked with a bitmap over the pool's ids: one
+// pass to mark, one to clear the words it marked, so a call costs O(n) however
+// large the pool (sorting 20,000 ids took ~1 ms).  The bitmap is per thread,
+// all clear between calls, and keeps the largest size it has been given (at
+// most 16 MiB).  Larger pools are checked with sorted copies.
+constexpr uint64_t kBitmapMaxIds = 1ull << 27;
+
+uint64_t* id_bitmap(uint64_t n_pool) {
+  thread_local std::vector<uint64_t> bits;
+  const size_t words = (n_pool + 63) / 64;
+  if (bits.size() < words) bits.assign(words, 0);
+  return bits.data();
+}
+inline uint64_t bit_of(int64_t id) { return 1ull << ((uint64_t)id & 63); }
+void clear_marks(uint64_t* bits, const int64_t* ids, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) bits[(uint64_t)ids[i] >> 6] = 0;
+}
+}  // namespace
+
+int check_unique(const int64_t* ids, int64_t n, uint64_t n_pool) {
+  if (n_pool <= kBitmapMaxIds) {
+    uint64_t* bits = id_bitmap(n_pool);
+    int rc = AEGKV_OK;
+    for (int64_t i = 0; i < n && rc == AEGKV_OK; ++i) {
+      uint64_t& w = bits[(uint64_t)ids[i] >> 6];
+      if (w & bit_of(ids[i])) rc = AEGKV_ERR_DUPLICATE;
+      w |= bit_of(ids[i]);
+    }
+    clear_marks(bits, ids, n);
+    return rc;
+  }
   std::vector<int64_t> v(ids, ids + n);
   std::sort(v.begin(), v.end());
   for (size_t i = 1; i < v.size(); ++i)
@@ -23,7 +54,16 @@ int check_unique(const int64_t* ids, int64_t n) {
   return AEGKV_OK;
 }
 
-int check_disjoint(const int64_t* a, int64_t na, const int64_t* b, int64_t nb) {
+int check_disjoint(const int64_t* a, int64_t na, const int64_t* b, int64_t nb, uint64_t n_pool) {
+  if (n_pool <= kBitmapMaxIds) {
+    uint64_t* bits = id_bitmap(n_pool);
+    for (int64_t i = 0; i < na; ++i) bits[(uint64_t)a[i] >> 6] |= bit_of(a[i]);
+    int rc = AEGKV_OK;
+    for (int64_t i = 0; i < nb && rc == AEGKV_OK; ++i)
+      if (bits[(uint64_t)b[i] >> 6] & bit_of(b[i])) rc = AEGKV_ERR_OVERLAP;
+    clear_marks(bits, a, na);
+    return rc;
+  }
   std::vector<int64_t> x(a, a + na), y(b, b + nb);
   std::sort(x.begin(), x.end());
   std::sort(y.begin(), y.end());

@@ -69,6 +69,20 @@ def test_block_copy_argument_checks(lib):
     assert lib.aegkv_defrag_blocks(pool, 64, None, dp, 3, 16, None) == INVALID
     assert lib.aegkv_pack_blocks(pool, 64, None, 3, pool, 16, None) == INVALID
     assert lib.aegkv_scatter_blocks(pool, badp, 3, pool, 64, 16, None) == RANGE
+    # the last id of the pool, repeated (the checks mark a bitmap over the pool)
+    top, topp = _i64([63, 62, 63])
+    assert lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, topp, 3, 16, None) == DUP
+    # a pool far larger than the lists: the checks sort copies instead
+    huge = 1 << 40
+    assert lib.aegkv_copy_blocks(pool, huge, pool, huge, sp, dupp, 3, 16, None) == DUP
+    assert lib.aegkv_copy_blocks(pool, huge, pool, huge, sp, sp, 3, 16, None) == OVERLAP
+    assert lib.aegkv_defrag_blocks(pool, huge, sp, sp, 3, 16, None) == OVERLAP
+    # the checks leave no marks behind: after the rejected calls above, lists
+    # that reuse their ids pass them (and the call then fails later, at the
+    # device query, as there is no GPU here)
+    ok, okp = _i64([6, 7, 63])
+    rc = lib.aegkv_copy_blocks(pool, 64, pool, 64, sp, okp, 3, 16, None)
+    assert rc not in (OK, DUP, OVERLAP, RANGE, INVALID, MISALIGNED), rc
 
 
 def test_swap_argument_checks(lib):
