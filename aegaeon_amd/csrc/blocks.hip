@@ -163,6 +163,9 @@ int copy_blocks_checked(const void* src_pool, uint64_t n_src_blocks, void* dst_p
   if (n == 0) return AEGKV_OK;
   if ((block_bytes & 15) || !aligned16(src_pool) || !aligned16(dst_pool))
     return AEGKV_ERR_MISALIGNED;
+  // pool byte sizes must be representable (they bound the overlap test)
+  if (n_src_blocks > UINT64_MAX / block_bytes || n_dst_blocks > UINT64_MAX / block_bytes)
+    return AEGKV_ERR_INVALID_ARG;
   int rc;
   if (src_ids) {
     if ((rc = check_ids_in_range(src_ids, n, n_src_blocks))) return rc;
@@ -259,6 +262,8 @@ int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
   if (n < 0 || !dev_pool || !host_pool || block_bytes == 0) return AEGKV_ERR_INVALID_ARG;
   if (n == 0) return AEGKV_OK;
   if (!src_ids || !dst_ids) return AEGKV_ERR_INVALID_ARG;
+  if (n_dev_blocks > UINT64_MAX / block_bytes || n_host_blocks > UINT64_MAX / block_bytes)
+    return AEGKV_ERR_INVALID_ARG;
   const uint64_t n_src = is_swap_in ? n_host_blocks : n_dev_blocks;
   const uint64_t n_dst = is_swap_in ? n_dev_blocks : n_host_blocks;
   int rc;
@@ -406,6 +411,8 @@ int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, in
     return AEGKV_ERR_INVALID_ARG;
   if (n == 0) return AEGKV_OK;
   if (!src_ids || !dst_ids) return AEGKV_ERR_INVALID_ARG;
+  if (n_dev_blocks > UINT64_MAX / block_bytes || n_host_blocks > UINT64_MAX / block_bytes)
+    return AEGKV_ERR_INVALID_ARG;
   const uint64_t n_src = is_swap_in ? n_host_blocks : n_dev_blocks;
   const uint64_t n_dst = is_swap_in ? n_dev_blocks : n_host_blocks;
   int rc;

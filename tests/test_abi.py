@@ -77,6 +77,8 @@ def test_block_copy_argument_checks(lib):
     assert lib.aegkv_copy_blocks(pool, huge, pool, huge, sp, dupp, 3, 16, None) == DUP
     assert lib.aegkv_copy_blocks(pool, huge, pool, huge, sp, sp, 3, 16, None) == OVERLAP
     assert lib.aegkv_defrag_blocks(pool, huge, sp, sp, 3, 16, None) == OVERLAP
+    # a pool whose byte size does not fit 64 bits
+    assert lib.aegkv_copy_blocks(pool, 1 << 62, pool + 4096, 64, sp, dp, 3, 16, None) == INVALID
     # the checks leave no marks behind: after the rejected calls above, lists
     # that reuse their ids pass them (and the call then fails later, at the
     # device query, as there is no GPU here)
@@ -99,6 +101,8 @@ def test_swap_argument_checks(lib):
     assert lib.aegkv_swap_blocks(sp, bigp, 2, 1, dev, 8, h, 8, 16, None, 0, None) == RANGE
     assert lib.aegkv_swap_blocks(sp, dupp, 2, 0, dev, 8, h, 8, 16, None, 0, None) == DUP
     assert lib.aegkv_swap_blocks(sp, sp, 2, 0, dev, 8, h, 8, 0, None, 0, None) == INVALID
+    # a host pool whose byte size does not fit 64 bits
+    assert lib.aegkv_swap_blocks(sp, sp, 2, 0, dev, 8, h, 1 << 62, 16, None, 0, None) == INVALID
 
 
 def test_append_and_gather_argument_checks(lib):
