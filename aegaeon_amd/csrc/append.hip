@@ -257,8 +257,11 @@ int aegkv_kv_append(const void* key, const void* value, int64_t key_token_stride
       ((value_layer_stride * e) & 15) || ((cache_block_stride * e) & 15) ||
       ((cache_layer_stride * e) & 15))
     return AEGKV_ERR_MISALIGNED;
-  const uint64_t total = (uint64_t)n_layers * 2 * (uint64_t)n_tokens * (uint64_t)(row_bytes / 16);
-  if (total >= (1ull << 32)) return AEGKV_ERR_UNSUPPORTED;
+  // chunks of the launch, counted in 128 bits so that no product wraps
+  const unsigned __int128 total128 = (unsigned __int128)(uint64_t)n_layers * 2 *
+                                     (uint64_t)n_tokens * (uint64_t)(row_bytes / 16);
+  if (total128 >= ((unsigned __int128)1 << 32)) return AEGKV_ERR_UNSUPPORTED;
+  const uint64_t total = (uint64_t)total128;
   AppendArgs a;
   a.key = static_cast<const uint8_t*>(key);
   a.value = static_cast<const uint8_t*>(value);
@@ -307,6 +310,7 @@ int aegkv_gather_tokens(const void* key_cache, const void* value_cache,
       !aligned16(out_key) || !aligned16(out_value) || ((cache_block_stride * e) & 15) ||
       ((cache_layer_stride * e) & 15) || ((out_layer_stride * e) & 15))
     return AEGKV_ERR_MISALIGNED;
+  if (row_bytes > INT32_MAX) return AEGKV_ERR_UNSUPPORTED;
   const int64_t blocks_needed = ((int64_t)max_seq_len + block_size - 1) / block_size;
   if (blocks_needed > max_blocks) return AEGKV_ERR_INVALID_ARG;
   const int64_t passes = ((int64_t)block_size * row_bytes + kGatherPassBytes - 1) / kGatherPassBytes;

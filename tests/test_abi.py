@@ -120,6 +120,7 @@ def test_append_and_gather_argument_checks(lib):
     assert append(key=mis) == MISALIGNED
     assert append(tok_stride=3) == MISALIGNED
     assert append(dim=3) == MISALIGNED  # 2*3*2 = 12-byte rows
+    assert append(n_tokens=1 << 62) == UNSUP  # 2^67 chunks: no product may wrap
     # gather: max_seq_len needs more blocks than the table is wide
     assert lib.aegkv_gather_tokens(p, p, 4096, 0, 4, p, 1, p, p, 2, 40, p, p, 80, 0, 1, 16, 2,
                                    64, 2, None) == INVALID
@@ -127,6 +128,9 @@ def test_append_and_gather_argument_checks(lib):
                                    64, 4, None) == UNSUP
     assert lib.aegkv_gather_tokens(p, p, 4096, 0, 4, p, 3, p, p, 0, 40, p, p, 80, 0, 1, 16, 2,
                                    64, 2, None) == OK
+    # rows wider than 2 GiB
+    assert lib.aegkv_gather_tokens(p, p, 4096, 0, 4, p, 3, p, p, 2, 40, p, p, 80, 0, 1, 16,
+                                   1 << 16, 1 << 16, 2, None) == UNSUP
     del args
 
 
