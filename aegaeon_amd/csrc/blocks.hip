@@ -33,20 +33,13 @@
 
 #include "aegkv_internal.h"
 
-#ifndef AEGKV_TILE_UNROLL
-#define AEGKV_TILE_UNROLL 1
-#endif
-
 namespace aegkv {
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-#ifndef AEGKV_COPY_THREADS
-#define AEGKV_COPY_THREADS 64
-#endif
-constexpr int kCopyThreads = AEGKV_COPY_THREADS;
-constexpr int kTileUnroll = AEGKV_TILE_UNROLL;  // dwordx4 per lane per tile: 1 KiB tiles
+constexpr int kCopyThreads = 64;  // one wave per workgroup
+constexpr int kTileUnroll = 1;    // dwordx4 per lane per tile: 1 KiB tiles
 // Stores: non-temporal with device scope (nt sc1).  Bench sections, same call,
 // two rounds, TB/s against nt alone: pack 6.51-6.52 / 6.38-6.48, scatter
 // 6.83-6.85 / 6.78-6.79, defrag 6.71-6.72 / 6.60, copy calibration 6.11 /
@@ -58,10 +51,7 @@ constexpr int kStorePolicy = kNt | 16;
 // 1 KiB tiles measured best there too (107 GB: 6.50-6.61 TB/s against
 // 6.07-6.32 for 4 KiB and 5.70-5.73 for 8 KiB; the 29.4 MB copy floor the
 // same within 0.1 us).
-#ifndef AEGKV_LINEAR_UNROLL
-#define AEGKV_LINEAR_UNROLL 1
-#endif
-constexpr int kLinearUnroll = AEGKV_LINEAR_UNROLL;
+constexpr int kLinearUnroll = 1;
 // Largest grid of one launch: HIP bounds a launch to 2^32 - 1 work-items per
 // dimension; a block of more tiles loops its grid row over the rest, and more
 // than kMaxCopyGridY blocks take several launches.
