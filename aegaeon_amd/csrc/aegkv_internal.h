@@ -34,7 +34,13 @@ int check_disjoint(const int64_t* a, int64_t na, const int64_t* b, int64_t nb, u
 // Per-device state: compute-unit count and the id upload ring.  Host id lists
 // are copied into a pinned host slice and DMA'd to the matching device slice on
 // the caller's stream; an event recorded after the consuming kernel guards the
-// slice until the device is done with it.
+// slice until the device is done with it.  When the next slice would overlap
+// one the device has not finished with, the ring grows (doubling, up to
+// kRingGrowMax elements) instead of waiting, so a caller that enqueues many
+// calls ahead of the device is not blocked; past that size it waits for the
+// overlapped slices.  A replaced ring stays allocated until the process ends
+// (its slices may still be read, and freeing device memory would synchronise
+// the device).
 struct DeviceState {
   int device = -1;
   int num_cu = 0;
@@ -48,9 +54,13 @@ struct DeviceState {
     size_t begin, end;
     hipEvent_t ev;
   };
-  std::deque<Span> inflight;
+  std::deque<Span> inflight;       // slices of the current ring
+  std::deque<hipEvent_t> retired;   // events of slices of replaced rings
+  std::vector<int64_t*> old_rings;  // replaced rings (host and device), kept
   std::vector<hipEvent_t> spare_events;
 };
+constexpr size_t kRingInitial = (size_t)1 << 17;  // elements (1 MiB each side)
+constexpr size_t kRingGrowMax = (size_t)1 << 22;  // elements (32 MiB each side)
 
 // State of the current device (created on first use).  Returns 0 or a status.
 int current_device_state(DeviceState** out);

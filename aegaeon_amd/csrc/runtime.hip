@@ -83,14 +83,28 @@ void release_span(DeviceState* ds, const DeviceState::Span& s) {
   ds->spare_events.push_back(s.ev);
 }
 
-int wait_all(DeviceState* ds) {
-  while (!ds->inflight.empty()) {
-    DeviceState::Span s = ds->inflight.front();
-    ds->inflight.pop_front();
-    hipError_t e = hipEventSynchronize(s.ev);
-    release_span(ds, s);
-    if (e != hipSuccess) return (int)e;
+// A new ring of at least `need` elements (doubling): the current one is kept
+// allocated and its unfinished slices move to the retired events.
+int ring_grow(DeviceState* ds, size_t need) {
+  const size_t cap = std::max<size_t>({need, 2 * ds->cap, kRingInitial});
+  int64_t* h = nullptr;
+  int64_t* d = nullptr;
+  AEGKV_HIP_TRY(hipHostMalloc((void**)&h, cap * sizeof(int64_t), hipHostMallocDefault));
+  hipError_t e = hipMalloc((void**)&d, cap * sizeof(int64_t));
+  if (e != hipSuccess) {
+    (void)hipHostFree(h);  // never handed out
+    return (int)e;
   }
+  if (ds->host_ring) {
+    ds->old_rings.push_back(ds->host_ring);
+    ds->old_rings.push_back(ds->dev_ring);
+  }
+  for (const auto& sp : ds->inflight) ds->retired.push_back(sp.ev);
+  ds->inflight.clear();
+  ds->host_ring = h;
+  ds->dev_ring = d;
+  ds->cap = cap;
+  ds->head = 0;
   return AEGKV_OK;
 }
 }  // namespace
@@ -119,38 +133,47 @@ int current_device_state(DeviceState** out) {
 }
 
 int ring_acquire(DeviceState* ds, size_t n, size_t* begin) {
-  if (n > ds->cap) {
-    // Grow: every slice of the old ring must be idle before it is freed.
-    int rc = wait_all(ds);
-    if (rc) return rc;
-    if (ds->host_ring) AEGKV_HIP_TRY(hipHostFree(ds->host_ring));
-    if (ds->dev_ring) AEGKV_HIP_TRY(hipFree(ds->dev_ring));
-    ds->host_ring = nullptr;
-    ds->dev_ring = nullptr;
-    size_t cap = std::max<size_t>({n, 2 * ds->cap, (size_t)1 << 17});
-    AEGKV_HIP_TRY(hipHostMalloc((void**)&ds->host_ring, cap * sizeof(int64_t), hipHostMallocDefault));
-    AEGKV_HIP_TRY(hipMalloc((void**)&ds->dev_ring, cap * sizeof(int64_t)));
-    ds->cap = cap;
-    ds->head = 0;
+  // Drop finished slices, of this ring and of replaced ones, oldest first (a
+  // slice finished behind an unfinished older one is dropped later).
+  while (!ds->inflight.empty() && hipEventQuery(ds->inflight.front().ev) == hipSuccess) {
+    release_span(ds, ds->inflight.front());
+    ds->inflight.pop_front();
   }
-  if (ds->head + n > ds->cap) ds->head = 0;
-  size_t b = ds->head, e = b + n;
-  // Wait for in-flight slices that overlap [b, e); drop finished ones.
-  for (auto it = ds->inflight.begin(); it != ds->inflight.end();) {
-    bool overlap = it->begin < e && b < it->end;
-    if (overlap) {
-      hipError_t err = hipEventSynchronize(it->ev);
-      release_span(ds, *it);
-      it = ds->inflight.erase(it);
-      if (err != hipSuccess) return (int)err;
-    } else if (hipEventQuery(it->ev) == hipSuccess) {
-      release_span(ds, *it);
-      it = ds->inflight.erase(it);
+  while (!ds->retired.empty() && hipEventQuery(ds->retired.front()) == hipSuccess) {
+    ds->spare_events.push_back(ds->retired.front());
+    ds->retired.pop_front();
+  }
+  if (n > ds->cap) {
+    int rc = ring_grow(ds, n);
+    if (rc) return rc;
+  }
+  size_t b = ds->head + n > ds->cap ? 0 : ds->head;
+  auto overlaps = [&](size_t lo) {
+    for (const auto& sp : ds->inflight)
+      if (sp.begin < lo + n && lo < sp.end) return true;
+    return false;
+  };
+  if (overlaps(b)) {
+    if (2 * ds->cap <= kRingGrowMax) {
+      // the device is still reading that slice: a larger ring, not a wait
+      int rc = ring_grow(ds, n);
+      if (rc) return rc;
+      b = 0;
     } else {
-      ++it;
+      // Wait for the overlapped slices (the ring is at its largest).
+      for (auto it = ds->inflight.begin(); it != ds->inflight.end();) {
+        if (it->begin < b + n && b < it->end) {
+          hipError_t err = hipEventSynchronize(it->ev);
+          release_span(ds, *it);
+          it = ds->inflight.erase(it);
+          if (err != hipSuccess) return (int)err;
+        } else {
+          ++it;
+        }
+      }
     }
   }
-  ds->head = e;
+  ds->head = b + n;
   *begin = b;
   return AEGKV_OK;
 }

@@ -387,3 +387,35 @@ def test_llama_swap_through_pinned_host(device, n_host):
     del pool, host, before
     torch.cuda.empty_cache()
     torch._C._host_emptyCache()
+
+
+def test_calls_enqueued_far_ahead_of_the_device(device):
+    """48 packs of 16384 ids each (six times the library's first id upload
+    ring) enqueued behind a held stream: the host does not wait for the device
+    (the ring grows instead of waiting for slices the device has not read),
+    and every pack reads its own ids."""
+    torch.cuda.synchronize()
+    n_blocks, n, calls = 1 << 20, 16384, 48
+    gen = torch.Generator(device=device).manual_seed(11)
+    pool = torch.randint(-2**31, 2**31 - 1, (n_blocks, 4), dtype=torch.int32, device=device,
+                         generator=gen)
+    rng = np.random.default_rng(11)
+    ids = [rng.choice(n_blocks, n, replace=False).astype(np.int64) for _ in range(calls)]
+    outs = torch.zeros((calls, n, 4), dtype=torch.int32, device=device)
+    # calibrate the spin, then hold the stream for about 300 ms
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    torch.cuda._sleep(1_000_000)
+    e1.record()
+    e1.synchronize()
+    cycles_per_ms = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(300 * cycles_per_ms))
+    held = torch.cuda.Event()
+    held.record()
+    for c in range(calls):
+        ops.pack_blocks(pool, ids[c], out=outs[c])
+    still_held = not held.query()
+    torch.cuda.synchronize()
+    for c in range(calls):
+        assert torch.equal(outs[c], pool[torch.from_numpy(ids[c]).to(device)]), c
+    assert still_held, "the host waited for the device while enqueueing"
