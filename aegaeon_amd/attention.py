@@ -81,6 +81,8 @@ def reshape_and_cache_flash(key: torch.Tensor, value: torch.Tensor, key_cache: t
     if key.dim() != 3 or value.shape != key.shape or key.shape[1:] != key_cache.shape[2:]:
         raise ValueError("key/value must be [T, Hkv, D] matching the cache view")
     T = key.size(0)
+    if slot_mapping.dim() != 1 or slot_mapping.numel() < T:
+        raise ValueError(f"slot_mapping must hold a slot for each of the {T} tokens")
     N, bs, H, D = key_cache.shape
     slot_mapping = slot_mapping.contiguous()
     with torch.cuda.device(key.device):
@@ -111,8 +113,10 @@ def append_kv(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
         _check_on(t, n, kv_cache.device)
     if key.dtype != kv_cache.dtype or value.dtype != kv_cache.dtype or key.element_size() != 2:
         raise ValueError("key, value and kv_cache must share one 16-bit dtype")
-    slot_mapping = slot_mapping.contiguous()
     T = key.size(1)
+    if slot_mapping.dim() != 1 or slot_mapping.numel() < T:
+        raise ValueError(f"slot_mapping must hold a slot for each of the {T} tokens")
+    slot_mapping = slot_mapping.contiguous()
     kv_stride = bs * H * D
     with torch.cuda.device(kv_cache.device):
         base = kv_cache.data_ptr()

@@ -71,6 +71,27 @@ def test_out_of_range_slots_skipped(device):
     assert np.array_equal(got, ref)
 
 
+def test_append_rejects_short_slot_mapping(device):
+    """A slot list shorter than the tokens (or not 1-d) raises before any
+    launch, for both the per-layer and the all-layer call; the cache is
+    untouched."""
+    rng = np.random.default_rng(6)
+    N, L, H, D = 8, 2, 2, 64
+    cache = to_device_bits(random_bits(rng, (N, L, 2, 16, H, D), "fp16"), "fp16", device)
+    before = to_bits(cache)
+    key = to_device_bits(random_bits(rng, (L, 4, H, D), "fp16"), "fp16", device)
+    val = to_device_bits(random_bits(rng, (L, 4, H, D), "fp16"), "fp16", device)
+    view = cache.permute(1, 2, 0, 3, 4, 5)
+    for slots in (torch.arange(3, dtype=torch.int64, device=device),
+                  torch.arange(4, dtype=torch.int64, device=device).view(2, 2)):
+        with pytest.raises(ValueError):
+            A.append_kv(key, val, cache, slots)
+        with pytest.raises(ValueError):
+            A.reshape_and_cache_flash(key[0], val[0], view[0, 0], view[0, 1], slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bits(cache), before)
+
+
 def test_qwen_full_size_append(device):
     """Qwen2.5-7B shape, 256 sequences, pool = 2x need (17.4 GB): each appended
     row reads back exactly (append -> gather identity) and no other byte
