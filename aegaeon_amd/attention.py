@@ -521,12 +521,15 @@ def varlen_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_cuda or cu_seqlens.dim() != 1 \
             or not cu_seqlens.is_contiguous():
         raise ValueError("cu_seqlens must be a contiguous int32 GPU tensor [batch + 1]")
+    for x, n in ((k, "k"), (v, "v"), (cu_seqlens, "cu_seqlens")):
+        _check_on(x, n, q.device)
     if out is None:
         out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
     elif out.shape != (T, Hq, D) or out.dtype != q.dtype:
         raise ValueError("out must be [tokens, Hq, D] of q's dtype")
     else:
         _check_rows(out, "out")
+        _check_on(out, "out", q.device)
     with torch.cuda.device(q.device):
         rc = _lib.load().aegkv_varlen_prefill_attention(
             out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0),
