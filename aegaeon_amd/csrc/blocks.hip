@@ -28,6 +28,8 @@
 // 5.33 TB/s, hipMemcpyAsync of a contiguous 1 GiB at 5.13.
 #include <algorithm>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <numeric>
 #include <thread>
 
@@ -387,6 +389,43 @@ void copy_bounce_chunk(void* user) {
   delete c;
 }
 
+// The stream that runs the host copies of bounced swaps, one per device
+// (default priority), so that a chunk's host copy overlaps the next chunk's
+// DMA on the caller's stream.
+int host_copy_stream(hipStream_t* out) {
+  static std::mutex mu;
+  static std::map<int, hipStream_t> streams;
+  int dev = 0;
+  AEGKV_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = streams.find(dev);
+  if (it == streams.end()) {
+    hipStream_t s = nullptr;
+    AEGKV_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    it = streams.emplace(dev, s).first;
+  }
+  *out = it->second;
+  return AEGKV_OK;
+}
+
+// Events of one bounced swap: created per call and released once enqueued (a
+// destroyed event that is still pending is released by the runtime when it
+// completes).
+struct EventList {
+  std::vector<hipEvent_t> ev;
+  ~EventList() {
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+  }
+  int record(hipStream_t s, hipEvent_t* out) {
+    hipEvent_t e = nullptr;
+    AEGKV_HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    ev.push_back(e);
+    AEGKV_HIP_TRY(hipEventRecord(e, s));
+    *out = e;
+    return AEGKV_OK;
+  }
+};
+
 }  // namespace
 
 extern "C" {
@@ -411,50 +450,87 @@ int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, in
   if ((rc = check_unique(dst_ids, n, n_dst))) return rc;
   const uint64_t bb = block_bytes;
   if ((bb & 15) || !aligned16(dev_pool) || !aligned16(staging)) return AEGKV_ERR_MISALIGNED;
-  const uint64_t cap64 = std::min(staging_bytes, bounce_bytes) / bb;
-  if (cap64 == 0) return AEGKV_ERR_WORKSPACE;
+  if (std::min(staging_bytes, bounce_bytes) / bb == 0) return AEGKV_ERR_WORKSPACE;
+  // The bounce buffer is cut into two halves when each holds a block and
+  // there is more than one chunk to move: chunk k uses half k % 2, so its
+  // host copy overlaps the next chunk's DMA, and half reuse waits for the
+  // chunk two back.
+  const uint64_t halves = (bounce_bytes / bb >= 2 && (uint64_t)n > 1) ? 2 : 1;
+  const uint64_t half_bytes = bounce_bytes / halves / bb * bb;
+  const int64_t cap =
+      (int64_t)std::min<uint64_t>({staging_bytes / bb, half_bytes / bb, (uint64_t)n});
   DeviceState* ds = nullptr;
   if ((rc = current_device_state(&ds))) return rc;
+  hipStream_t hs = nullptr;  // host copies
+  if ((rc = host_copy_stream(&hs))) return rc;
   uint8_t* dev = static_cast<uint8_t*>(dev_pool);
   uint8_t* host = static_cast<uint8_t*>(host_pool);
   uint8_t* stg = static_cast<uint8_t*>(staging);
-  uint8_t* bnc = static_cast<uint8_t*>(bounce);
-  const int64_t cap = (int64_t)std::min<uint64_t>(cap64, (uint64_t)n);
   const int64_t* dev_key = is_swap_in ? dst_ids : src_ids;
   const int64_t* host_key = is_swap_in ? src_ids : dst_ids;
-  for (int64_t c0 = 0; c0 < n; c0 += cap) {
+  EventList events;
+  std::vector<hipEvent_t> done;  // per chunk: its half may be reused after this
+  hipEvent_t ev = nullptr;
+  if (is_swap_in) {
+    // the host reads the file after the caller's earlier work on its stream
+    if ((rc = events.record(stream, &ev))) return rc;
+    AEGKV_HIP_TRY(hipStreamWaitEvent(hs, ev, 0));
+  }
+  for (int64_t c0 = 0, k = 0; c0 < n; c0 += cap, ++k) {
     const int64_t m = std::min(cap, n - c0);
+    uint8_t* half = static_cast<uint8_t*>(bounce) + (uint64_t)(k % (int64_t)halves) * half_bytes;
     BounceChunk* chunk = nullptr;
     try {
-      chunk = new BounceChunk{bnc, host, bb, !is_swap_in,
+      chunk = new BounceChunk{half, host, bb, !is_swap_in,
                               std::vector<int64_t>(host_key + c0, host_key + c0 + m)};
     } catch (...) {
       return AEGKV_ERR_RUNTIME;
     }
     IdPart part{dev_key + c0, m};
+    const bool reuse = k >= (int64_t)halves;  // the half held chunk k - halves
     if (!is_swap_in) {
-      // pack the device blocks, DMA them to the bounce buffer, then the host
-      // copies them into the pool's blocks (the next chunk's DMA waits for it)
+      // pack the device blocks and DMA them to the half (once its previous
+      // host copy is done); the host copy stream then writes them to the pool
       rc = with_uploaded_ids(ds, stream, &part, 1, [&](int64_t* ids) {
         return launch_copy_blocks(ds, dev, stg, ids, nullptr, m, bb, stream);
       });
-      if (rc) { delete chunk; return rc; }
-      hipError_t e = hipMemcpyAsync(bnc, stg, (uint64_t)m * bb, hipMemcpyDeviceToHost, stream);
-      if (e != hipSuccess) { delete chunk; return (int)e; }
-      e = hipLaunchHostFunc(stream, copy_bounce_chunk, chunk);
-      if (e != hipSuccess) { delete chunk; return (int)e; }
+      hipError_t e = hipSuccess;
+      if (!rc && reuse) e = hipStreamWaitEvent(stream, done[k - halves], 0);
+      if (!rc && e == hipSuccess)
+        e = hipMemcpyAsync(half, stg, (uint64_t)m * bb, hipMemcpyDeviceToHost, stream);
+      if (!rc && e == hipSuccess) rc = events.record(stream, &ev);
+      if (!rc && e == hipSuccess) e = hipStreamWaitEvent(hs, ev, 0);
+      if (!rc && e == hipSuccess) e = hipLaunchHostFunc(hs, copy_bounce_chunk, chunk);
+      if (rc || e != hipSuccess) {
+        delete chunk;
+        return rc ? rc : (int)e;
+      }
+      if ((rc = events.record(hs, &ev))) return rc;
+      done.push_back(ev);
     } else {
-      // the host gathers the pool's blocks into the bounce buffer, one DMA
-      // takes them to staging, and the scatter kernel places them
-      hipError_t e = hipLaunchHostFunc(stream, copy_bounce_chunk, chunk);
-      if (e != hipSuccess) { delete chunk; return (int)e; }
-      AEGKV_HIP_TRY(hipMemcpyAsync(stg, bnc, (uint64_t)m * bb, hipMemcpyHostToDevice, stream));
+      // the host gathers the pool's blocks into the half (once the DMA of its
+      // previous chunk is done), then one DMA takes them to staging and the
+      // scatter kernel places them
+      hipError_t e = hipSuccess;
+      if (reuse) e = hipStreamWaitEvent(hs, done[k - halves], 0);
+      if (e == hipSuccess) e = hipLaunchHostFunc(hs, copy_bounce_chunk, chunk);
+      if (e != hipSuccess) {
+        delete chunk;
+        return (int)e;
+      }
+      if ((rc = events.record(hs, &ev))) return rc;
+      AEGKV_HIP_TRY(hipStreamWaitEvent(stream, ev, 0));
+      AEGKV_HIP_TRY(hipMemcpyAsync(stg, half, (uint64_t)m * bb, hipMemcpyHostToDevice, stream));
+      if ((rc = events.record(stream, &ev))) return rc;
+      done.push_back(ev);
       rc = with_uploaded_ids(ds, stream, &part, 1, [&](int64_t* ids) {
         return launch_copy_blocks(ds, stg, dev, nullptr, ids, m, bb, stream);
       });
       if (rc) return rc;
     }
   }
+  // the caller's stream passes the swap-out only once its last host copy ran
+  if (!is_swap_in) AEGKV_HIP_TRY(hipStreamWaitEvent(stream, done.back(), 0));
   return AEGKV_OK;
 }
 

@@ -60,8 +60,9 @@ def init_cpu_cache(cpu_num_slabs: int, cpu_slab_size_bytes: int,
 
 
 def bounce_buffer(nbytes: int) -> torch.Tensor:
-    """A pinned host buffer for :func:`aegaeon_amd.ops.swap`'s ``bounce=``; a
-    swap moves min(staging, bounce) bytes per chunk."""
+    """A pinned host buffer for :func:`aegaeon_amd.ops.swap`'s ``bounce=``.  A
+    swap uses it as two halves (one chunk's host copy overlaps the next chunk's
+    DMA) and moves min(staging, half the bounce buffer) bytes per chunk."""
     return torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
 
 
