@@ -85,6 +85,50 @@ def test_swap_through_file_mapping(device, shm_path, bounce_blocks, staging_bloc
                           ref_host)
 
 
+def test_swaps_on_two_streams_through_one_file(device, shm_path):
+    """Two swap-outs into disjoint parts of the file, enqueued on two streams
+    behind a held stream, then two swap-ins back on the two streams: the
+    library's host-copy stream serves both calls, and its event ordering
+    keeps each chunk's halves apart and each swap-in after its own stream's
+    swap-out."""
+    rng = np.random.default_rng(21)
+    kv_swap = swap_pool.init_cpu_cache(N_SLABS, SLAB, shm_path)
+    n_host = kv_swap.numel() * 2 // BB
+    N = 96
+    bits = _seeded(7, N)
+    cache = bits.view(torch.bfloat16).to(device)
+    perm = rng.permutation(N)
+    src = [perm[:24], perm[24:48]]
+    hperm = rng.permutation(n_host)
+    host_ids = [hperm[:24], hperm[24:48]]
+    back = [perm[48:72], perm[72:96]]
+    streams = [torch.cuda.Stream(device), torch.cuda.Stream(device)]
+    bounces = [swap_pool.bounce_buffer(4 * BB), swap_pool.bounce_buffer(5 * BB)]
+    stagings = [torch.empty(3 * BB, dtype=torch.uint8, device=device) for _ in range(2)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(50_000_000)  # both streams start behind this hold
+    held = torch.cuda.Event()
+    held.record()
+    for i in range(2):
+        streams[i].wait_event(held)
+        with torch.cuda.stream(streams[i]):
+            ops.swap(src[i], host_ids[i], False, cache, kv_swap, staging=stagings[i],
+                     bounce=bounces[i])
+    for i in range(2):
+        with torch.cuda.stream(streams[i]):
+            ops.swap(host_ids[i], back[i], True, cache, kv_swap, staging=stagings[i],
+                     bounce=bounces[i])
+    torch.cuda.synchronize()
+    ref_gpu = bits.numpy().view(np.uint16).copy()
+    ref_host = np.zeros((n_host, *SHAPE), dtype=np.uint16)
+    for i in range(2):
+        ko.swap_blocks(src[i], host_ids[i], False, ref_gpu, ref_host)
+        ko.swap_blocks(host_ids[i], back[i], True, ref_gpu, ref_host)
+    assert np.array_equal(cache.view(torch.int16).cpu().numpy().view(np.uint16), ref_gpu)
+    got_host = kv_swap.view(torch.int16).numpy().view(np.uint16).reshape(ref_host.shape)
+    assert np.array_equal(got_host, ref_host)
+
+
 def test_pageable_swap_space_needs_a_bounce_buffer(device, shm_path):
     kv_swap = swap_pool.init_cpu_cache(N_SLABS, SLAB, shm_path)
     cache = torch.zeros((4, *SHAPE), dtype=torch.bfloat16, device=device)
