@@ -419,3 +419,32 @@ def test_calls_enqueued_far_ahead_of_the_device(device):
     for c in range(calls):
         assert torch.equal(outs[c], pool[torch.from_numpy(ids[c]).to(device)]), c
     assert still_held, "the host waited for the device while enqueueing"
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_id_lists_of_random_sizes_through_the_upload_ring(device, seed):
+    """Packs and scatters with id lists of random sizes (1 to 60,000 ids),
+    some enqueued behind a held stream and some not, so the upload ring wraps,
+    grows and reuses slices the device has released: every call reads its own
+    ids (checked against torch's gather and scatter of the same lists)."""
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(seed)
+    n_blocks = 1 << 18
+    gen = torch.Generator(device=device).manual_seed(seed)
+    pool = torch.randint(-2**31, 2**31 - 1, (n_blocks, 4), dtype=torch.int32, device=device,
+                         generator=gen)
+    sizes = rng.integers(1, 60_000, size=40)
+    ids = [rng.choice(n_blocks, int(k), replace=False).astype(np.int64) for k in sizes]
+    outs = [torch.zeros((int(k), 4), dtype=torch.int32, device=device) for k in sizes]
+    dst = torch.zeros_like(pool)
+    for c in range(len(ids)):
+        if c % 10 == 0:  # every tenth call starts behind a short hold
+            torch.cuda._sleep(2_000_000)
+        ops.pack_blocks(pool, ids[c], out=outs[c])
+        ops.scatter_blocks(outs[c], ids[c], dst)
+    torch.cuda.synchronize()
+    for c in range(len(ids)):
+        t = torch.from_numpy(ids[c]).to(device)
+        assert torch.equal(outs[c], pool[t]), c
+    touched = torch.from_numpy(np.unique(np.concatenate(ids))).to(device)
+    assert torch.equal(dst[touched], pool[touched])
