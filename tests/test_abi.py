@@ -105,6 +105,36 @@ def test_swap_argument_checks(lib):
     assert lib.aegkv_swap_blocks(sp, sp, 2, 0, dev, 8, h, 1 << 62, 16, None, 0, None) == INVALID
 
 
+def test_bounced_swap_argument_checks(lib):
+    raw, dev = _buf(16 * 8)
+    host = np.zeros(16 * 8, dtype=np.uint8)
+    h = host.ctypes.data
+    rawb, bnc = _buf(16 * 4)
+    raws, stg = _buf(16 * 4)
+    s, sp = _i64([0, 1])
+    big, bigp = _i64([0, 8])
+    dup, dupp = _i64([2, 2])
+    sw = lib.aegkv_swap_blocks_bounced
+
+    def call(src=sp, dst=sp, n=2, swap_in=0, dev_=dev, n_dev=8, n_host=8, bb=16, staging=stg,
+             stg_bytes=64, bounce=bnc, bounce_bytes=64):
+        return sw(src, dst, n, swap_in, dev_, n_dev, h, n_host, bb, staging, stg_bytes, bounce,
+                  bounce_bytes, None)
+
+    assert call(n=-1) == INVALID
+    assert call(n=0) == OK
+    assert call(bounce=None) == INVALID
+    assert call(staging=None) == INVALID
+    assert call(src=None) == INVALID
+    assert call(src=bigp) == RANGE
+    assert call(dst=bigp, swap_in=1) == RANGE
+    assert call(dst=dupp) == DUP
+    assert call(bb=24) == MISALIGNED
+    assert call(bounce_bytes=8) == WS       # the bounce buffer holds no block
+    assert call(stg_bytes=8) == WS          # nor does the staging buffer
+    assert call(n_host=1 << 62) == INVALID  # a pool whose byte size does not fit 64 bits
+
+
 def test_append_and_gather_argument_checks(lib):
     raw, p = _buf(4096)
     raw2, mis = _buf(4096, misalign=2)
