@@ -378,14 +378,21 @@ void copy_bounce_chunk(void* user) {
       off += len;
     }
   };
-  if (nt == 1) {
-    work(0);
-  } else {
-    std::vector<std::thread> th;
-    for (int t = 1; t < nt; ++t) th.emplace_back(work, t);
-    work(0);
-    for (auto& x : th) x.join();
+  // Shares no thread could be started for (thread creation failing) are
+  // copied here, so the callback never throws.
+  std::vector<std::thread> th;
+  int started = 1;
+  for (int t = 1; t < nt; ++t) {
+    try {
+      th.emplace_back(work, t);
+      ++started;
+    } catch (...) {
+      break;
+    }
   }
+  for (int t = started; t < nt; ++t) work(t);
+  work(0);
+  for (auto& x : th) x.join();
   delete c;
 }
 
