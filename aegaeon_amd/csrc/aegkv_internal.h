@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <deque>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include "../../include/aegkv.h"
@@ -21,6 +22,19 @@ namespace aegkv {
 
 inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Runs an entry point's body so that no exception crosses the C ABI: a failed
+// host allocation returns AEGKV_ERR_HOST_MEMORY.
+template <typename F>
+int guarded(F&& body) {
+  try {
+    return body();
+  } catch (const std::bad_alloc&) {
+    return AEGKV_ERR_HOST_MEMORY;
+  } catch (...) {
+    return AEGKV_ERR_HOST_MEMORY;  // std::length_error and the like from the containers
+  }
 }
 
 // Host-side validation of an id list against a pool of n_pool blocks.

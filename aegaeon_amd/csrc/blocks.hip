@@ -147,7 +147,7 @@ bool ranges_overlap(const void* a, uint64_t na, const void* b, uint64_t nb) {
 
 // Shared body of copy/pack/scatter/defrag: validate on the host, upload the id
 // lists, launch one copy kernel.
-int copy_blocks_checked(const void* src_pool, uint64_t n_src_blocks, void* dst_pool,
+int copy_blocks_checked_body(const void* src_pool, uint64_t n_src_blocks, void* dst_pool,
                         uint64_t n_dst_blocks, const int64_t* src_ids,
                         const int64_t* dst_ids, int64_t n, uint64_t block_bytes,
                         bool require_same_pool, hipStream_t stream) {
@@ -191,6 +191,16 @@ int copy_blocks_checked(const void* src_pool, uint64_t n_src_blocks, void* dst_p
     const int64_t* s = src_ids ? dev : nullptr;
     const int64_t* d = dst_ids ? dev + (src_ids ? n : 0) : nullptr;
     return launch_copy_blocks(ds, src_pool, dst_pool, s, d, n, block_bytes, stream);
+  });
+}
+
+int copy_blocks_checked(const void* src_pool, uint64_t n_src_blocks, void* dst_pool,
+                        uint64_t n_dst_blocks, const int64_t* src_ids,
+                        const int64_t* dst_ids, int64_t n, uint64_t block_bytes,
+                        bool require_same_pool, hipStream_t stream) {
+  return guarded([&] {
+    return copy_blocks_checked_body(src_pool, n_src_blocks, dst_pool, n_dst_blocks, src_ids,
+                                    dst_ids, n, block_bytes, require_same_pool, stream);
   });
 }
 
@@ -246,7 +256,7 @@ int aegkv_defrag_blocks(void* pool, uint64_t n_pool_blocks, const int64_t* src_i
                              block_bytes, true, (hipStream_t)stream);
 }
 
-int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+static int aegkv_swap_blocks_body(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
                       int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
                       void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
                       void* staging, uint64_t staging_bytes, aegkv_stream_t stream_) {
@@ -339,6 +349,17 @@ int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
     }
   }
   return AEGKV_OK;
+}
+
+int aegkv_swap_blocks(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+                      int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
+                      void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
+                      void* staging, uint64_t staging_bytes, aegkv_stream_t stream) {
+  return guarded([&] {
+    return aegkv_swap_blocks_body(src_ids, dst_ids, n, is_swap_in, dev_pool, n_dev_blocks,
+                                  host_pool, n_host_blocks, block_bytes, staging, staging_bytes,
+                                  stream);
+  });
 }
 
 }  // extern "C"
@@ -437,7 +458,7 @@ struct EventList {
 
 extern "C" {
 
-int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+static int aegkv_swap_blocks_bounced_body(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
                               int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
                               void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
                               void* staging, uint64_t staging_bytes, void* bounce,
@@ -539,6 +560,18 @@ int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, in
   // the caller's stream passes the swap-out only once its last host copy ran
   if (!is_swap_in) AEGKV_HIP_TRY(hipStreamWaitEvent(stream, done.back(), 0));
   return AEGKV_OK;
+}
+
+int aegkv_swap_blocks_bounced(const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+                              int is_swap_in, void* dev_pool, uint64_t n_dev_blocks,
+                              void* host_pool, uint64_t n_host_blocks, uint64_t block_bytes,
+                              void* staging, uint64_t staging_bytes, void* bounce,
+                              uint64_t bounce_bytes, aegkv_stream_t stream) {
+  return guarded([&] {
+    return aegkv_swap_blocks_bounced_body(src_ids, dst_ids, n, is_swap_in, dev_pool,
+                                          n_dev_blocks, host_pool, n_host_blocks, block_bytes,
+                                          staging, staging_bytes, bounce, bounce_bytes, stream);
+  });
 }
 
 }  // extern "C"

@@ -78,7 +78,7 @@ using namespace aegkv;
 
 extern "C" {
 
-int aegkv_prepare_inputs(const int32_t* block_ids, const int64_t* table_offsets,
+static int aegkv_prepare_inputs_body(const int32_t* block_ids, const int64_t* table_offsets,
                          const int32_t* seq_lens, const int32_t* context_lens,
                          const int64_t* tokens, int32_t batch, int32_t block_size,
                          int32_t pad_width, int32_t* block_tables_out,
@@ -162,6 +162,24 @@ int aegkv_prepare_inputs(const int32_t* block_ids, const int64_t* table_offsets,
     hipLaunchKernelGGL(prepare_inputs_kernel, dim3(gx, batch), dim3(kPrepThreads), 0, stream, a);
     AEGKV_HIP_TRY(hipGetLastError());
     return AEGKV_OK;
+  });
+}
+
+int aegkv_prepare_inputs(const int32_t* block_ids, const int64_t* table_offsets,
+                         const int32_t* seq_lens, const int32_t* context_lens,
+                         const int64_t* tokens, int32_t batch, int32_t block_size,
+                         int32_t pad_width, int32_t* block_tables_out,
+                         int64_t* slot_mapping_out, int64_t* positions_out,
+                         int64_t* input_tokens_out, int32_t* seq_lens_out,
+                         int32_t* context_lens_out, int32_t* query_start_loc_out,
+                         int32_t* seq_start_loc_out, int64_t n_query_tokens,
+                         aegkv_stream_t stream) {
+  return guarded([&] {
+    return aegkv_prepare_inputs_body(block_ids, table_offsets, seq_lens, context_lens, tokens,
+                                     batch, block_size, pad_width, block_tables_out,
+                                     slot_mapping_out, positions_out, input_tokens_out,
+                                     seq_lens_out, context_lens_out, query_start_loc_out,
+                                     seq_start_loc_out, n_query_tokens, stream);
   });
 }
 

@@ -226,6 +226,7 @@ const char* aegkv_strerror(int code) {
     case AEGKV_ERR_IN_USE: return "aegkv: request lives elsewhere, is held by a suspended call, or the space still holds requests";
     case AEGKV_RECLAIM_PENDING: return "aegkv: the call is suspended until pending moves are reclaimed (aegkv_bm_pending / aegkv_bm_resume)";
     case AEGKV_ERR_SCRATCH: return "aegkv: the call needs a larger workspace than the 32 MiB the no-allocation entry point holds";
+    case AEGKV_ERR_HOST_MEMORY: return "aegkv: a host-side allocation (id lists, bookkeeping) failed";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);

@@ -48,6 +48,7 @@ typedef void* aegkv_stream_t; /* hipStream_t */
 #define AEGKV_ERR_UNSUPPORTED (-6)   /* shape/dtype the kernels do not cover     */
 #define AEGKV_ERR_WORKSPACE (-7)     /* workspace/staging smaller than required  */
 #define AEGKV_ERR_RUNTIME (-8)       /* a HIP runtime query failed while sizing  */
+#define AEGKV_ERR_HOST_MEMORY (-13)  /* a host-side allocation failed           */
 
 /* dtype codes for the K/V and query elements */
 #define AEGKV_DTYPE_BF16 0
